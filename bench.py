@@ -1,0 +1,199 @@
+"""Benchmark of the denoiser attention block hot path on one MI355X.
+
+One step = one pass of the hot path at the 4608-token Boogu Turbo shape over resident synthetic
+inputs: the four packed-Q4 projection GEMMs (M 4608; K x N = 3072x9216 QKV, 3072x3072 O,
+3072x12288 MLP up, 12288x3072 MLP down; bf16 activations, f32 outputs) and the joint flash
+attention (B1 H24 S4608 D128, bf16 Q/K/V, f32 output).  Prints one JSON line.
+
+    python bench.py [--steps 20] [--warmup 3] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+M_TOKENS = 4608
+GEMMS = [("qkv", 3072, 9216), ("o", 3072, 3072), ("mlp_up", 3072, 12288), ("mlp_down", 12288, 3072)]
+ATTN = dict(B=1, H=24, S=4608, D=128)
+
+
+def gemm_flops(M, K, N):
+    return 2.0 * M * K * N
+
+
+def attn_flops(B, H, S, D):
+    return 4.0 * B * H * D * S * S
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-rows", type=int, default=1152,
+                    help="query rows / activation rows of the bounded CPU sample")
+    return ap.parse_args()
+
+
+def cpu_baseline(args, words_np, scales_np, x_np, q_np, k_np, v_np):
+    """Restated Burn NdArray CPU path on a bounded sample of the same workload: the four Q4
+    GEMMs over the first `cpu_rows` activation rows (dequantise + f32 matmul) and the joint
+    attention over the first `cpu_rows` query rows of every head (query-chunked f32 softmax).
+    Each op's rate is measured; the full step's CPU time is extrapolated op by op."""
+    from oracle import oracle as O
+    O.build()
+    rows = args.cpu_rows
+    t_total = 0.0
+    threads = 1
+    detail = {}
+    for (name, K, N) in GEMMS:
+        xs = np.ascontiguousarray(x_np[name][:rows])
+        t0 = time.perf_counter()
+        _, threads = O.cpu_q4_linear_f32(xs, words_np[name], scales_np[name], 1, 128, N)
+        dt = time.perf_counter() - t0
+        rate = gemm_flops(rows, K, N) / dt
+        detail[name] = rate / 1e12
+        t_total += gemm_flops(M_TOKENS, K, N) / rate
+    t0 = time.perf_counter()
+    O.cpu_attention_f32(q_np, k_np, v_np, requested_chunk=8192, q_rows=rows)
+    dt = time.perf_counter() - t0
+    rate = (4.0 * ATTN["H"] * ATTN["D"] * rows * ATTN["S"]) / dt
+    detail["attention"] = rate / 1e12
+    t_total += attn_flops(**ATTN) / rate
+    step_flops = sum(gemm_flops(M_TOKENS, K, N) for _, K, N in GEMMS) + attn_flops(**ATTN)
+    return {
+        "value": step_flops / t_total / 1e12,
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"restated Burn NdArray CPU path (dequantise + f32 matmul; query-chunked f32 "
+                   f"attention, chunk policy of attention.rs:36-45) on the first {rows} of 4608 "
+                   f"rows of each Q4 GEMM and {rows} query rows x 24 heads of the attention; "
+                   f"per-op rates extrapolated to one full step"),
+        "per_op_tflops": {k: round(v, 5) for k, v in detail.items()},
+        "ms_per_step": t_total * 1e3,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the hot path is measured on "
+                                   "a single MI355X; --gpus above 1 is not supported"}))
+        sys.exit(2)
+    import torch
+
+    import burn_image_amd as B
+    from burn_image_amd import workloads as W
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    gen = torch.Generator(device=dev).manual_seed(1234)
+
+    # ---------------- resident synthetic inputs -------------------------------------------
+    weights, xs, outs = {}, {}, {}
+    words_np, scales_np, x_np = {}, {}, {}
+    for i, (name, K, N) in enumerate(GEMMS):
+        wn, sn = W.q4_weight(3, 2 * i + 1, K, N, layout=1)
+        words_np[name], scales_np[name] = wn, sn
+        weights[name] = B.from_packed(torch.from_numpy(wn.view(np.int32)).to(dev),
+                                      torch.from_numpy(sn).to(dev), 1, 128, (K, N))
+        xn = W.activations(3, 2 * i, M_TOKENS, K, "bf16")
+        x_np[name] = xn
+        xs[name] = torch.from_numpy(xn).to(torch.bfloat16).to(dev)
+        outs[name] = torch.empty((M_TOKENS, N), dtype=torch.float32, device=dev)
+    q_np, k_np, v_np = W.boogu_attention(2)
+    q, k, v = (torch.from_numpy(a).to(torch.bfloat16).to(dev) for a in (q_np, k_np, v_np))
+    o = torch.empty((1, 24, 4608, 128), dtype=torch.float32, device=dev)
+
+    ops = [(name, (lambda n=name: B.q_matmul(xs[n], weights[n], out=outs[n]))) for name, _, _ in GEMMS[:1]]
+    ops.append(("attention", lambda: B.attention(q, k, v, out=o)))
+    ops += [(name, (lambda n=name: B.q_matmul(xs[n], weights[n], out=outs[n]))) for name, _, _ in GEMMS[1:]]
+    flops = {name: gemm_flops(M_TOKENS, K, N) for name, K, N in GEMMS}
+    flops["attention"] = attn_flops(**ATTN)
+    step_flops = sum(flops.values())
+
+    for _ in range(args.warmup):
+        for _, fn in ops:
+            fn()
+    torch.cuda.synchronize()
+
+    # ---------------- timed region: K steps, events around every launch --------------------
+    stream = torch.cuda.current_stream(dev)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(ops) + 1)] for _ in range(args.steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for s in range(args.steps):
+        evs[s][0].record(stream)
+        for j, (_, fn) in enumerate(ops):
+            fn()
+            evs[s][j + 1].record(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    per_op_ms = {name: float(np.mean([evs[s][j].elapsed_time(evs[s][j + 1]) for s in range(args.steps)]))
+                 for j, (name, _) in enumerate(ops)}
+
+    gemm_ms = sum(per_op_ms[n] for n, _, _ in GEMMS)
+    gemm_fl = sum(flops[n] for n, _, _ in GEMMS)
+    attn_ms = per_op_ms["attention"]
+    per_kernel = {n: {"ms": round(per_op_ms[n], 4),
+                      "tflops": round(flops[n] / (per_op_ms[n] * 1e-3) / 1e12, 2),
+                      "frac_peak": round(flops[n] / (per_op_ms[n] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+                  for n in per_op_ms}
+    if gemm_ms >= attn_ms:
+        dom, dom_fl, dom_ms, dom_launches = "q4_gemm", gemm_fl, gemm_ms, len(GEMMS)
+    else:
+        dom, dom_fl, dom_ms, dom_launches = "attention", flops["attention"], attn_ms, 1
+    achieved = dom_fl / (dom_ms * 1e-3) / 1e12
+    # Denoise block (block.rs:84-134 via feed_forward.rs:32-36): QKV + attention + O + two SwiGLU
+    # up projections + down projection, from the measured kernel times (glue kernels excluded).
+    block_ms = per_op_ms["qkv"] + attn_ms + per_op_ms["o"] + 2 * per_op_ms["mlp_up"] + per_op_ms["mlp_down"]
+
+    result = {
+        "metric": "attn + Q4-GEMM TFLOP/s and % MFMA peak @4608-tok DiT; ms per denoise block",
+        "value": round(step_flops / (ms_per_step * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "boogu-turbo-1024px-4608tok: Q4 QKV/O/MLP-up/MLP-down GEMMs "
+                               "(M4608, hidden 3072, block-128 f32 scales, bf16 activations) + "
+                               "joint attention B1 H24 S4608 D128 bf16",
+                   "tokens": M_TOKENS, "hidden": 3072, "heads": 24, "head_dim": 128,
+                   "parallelism": "single-gpu"},
+        "frac_peak": round(step_flops / (ms_per_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "ms_per_denoise_block": round(block_ms, 4),
+        "ms_per_denoise_block_1xup": round(block_ms - per_op_ms["mlp_up"], 4),
+        "per_kernel": per_kernel,
+        "roofline": {"bound": "mfma", "kernel": dom, "launches_per_step": dom_launches,
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args, words_np, scales_np, x_np, q_np, k_np, v_np)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

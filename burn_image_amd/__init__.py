@@ -1,0 +1,22 @@
+"""MI355X-native (gfx950) denoiser attention block of burn_image: packed signed-Q4 projection
+GEMMs and exact flash attention, as hand-written HIP kernels behind a C ABI (include/biq.h,
+libbiq.so), with a host-side mirror of the reference's Burn-facing operator surface."""
+from . import _lib
+from ._lib import BiqError, InvalidArgument, Unsupported, version
+from .attention import (AttentionKernel, NativeQ4FlashAttention, attention,
+                        effective_portable_query_chunk_size)
+from .linear import Linear, linear_forward, q_matmul, qwen_linear_forward
+from .q4 import (BOOGU_DENOISER, FLUX_VAE, QWEN3_VL, Q4Weight, from_packed,
+                 q4s_storage_block_and_axis, q4s_stored_dtype, quantize_q4s_block128_f32,
+                 quantize_row_layout_q4s_block_up_to128_f32)
+
+Q4_KN_AXIS1 = _lib.Q4_KN_AXIS1
+Q4_NK_AXIS0 = _lib.Q4_NK_AXIS0
+
+__all__ = [
+    "AttentionKernel", "NativeQ4FlashAttention", "attention", "effective_portable_query_chunk_size",
+    "Linear", "linear_forward", "q_matmul", "qwen_linear_forward", "Q4Weight", "from_packed",
+    "q4s_storage_block_and_axis", "q4s_stored_dtype", "quantize_q4s_block128_f32",
+    "quantize_row_layout_q4s_block_up_to128_f32", "BiqError", "InvalidArgument", "Unsupported",
+    "version", "BOOGU_DENOISER", "QWEN3_VL", "FLUX_VAE", "Q4_KN_AXIS1", "Q4_NK_AXIS0",
+]

@@ -1,0 +1,130 @@
+"""Flash attention on libbiq's HIP kernel, behind the reference's AttentionKernel seam.
+
+Mirrors crates/burn_boogu/src/model/attention.rs:47-135 (``AttentionKernel``: ``execute``,
+``execute_gqa``, ``execute_gqa_with_qk_norm_rope``, ``SPLIT_DOUBLE_STREAM_SHARED_PROJECTION``)
+and Burn's attention op (patches/burn-cubecl-0.21.0/src/ops/module.rs:342-367).  All arithmetic
+runs in libbiq; a missing library raises.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16,
+               torch.bfloat16: _lib.DTYPE_BF16}
+
+DEFAULT_QUERY_CHUNK_SIZE = 128
+PORTABLE_ATTENTION_MINIMUM_IMAGE_QUERY_PARTITIONS = 4
+
+
+def effective_portable_query_chunk_size(query_len: int, requested: int) -> int:
+    """attention.rs:36-45: cap a requested portable tile so image-scale queries stay partitioned."""
+    if requested <= 0:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention query chunk must be non-zero")
+    if query_len <= 0:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention query sequence must be non-empty")
+    if query_len <= DEFAULT_QUERY_CHUNK_SIZE:
+        return min(requested, query_len)
+    cap = -(-query_len // PORTABLE_ATTENTION_MINIMUM_IMAGE_QUERY_PARTITIONS)
+    return min(requested, max(cap, DEFAULT_QUERY_CHUNK_SIZE))
+
+
+def _strides_bhsd(t: torch.Tensor, name: str):
+    if t.dim() != 4:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, f"attention {name} must be rank 4")
+    if t.stride(3) != 1:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, f"attention {name} head width must be contiguous")
+    return _lib.strides3((t.stride(0), t.stride(1), t.stride(2)))
+
+
+def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *,
+              is_causal: bool = False, scale: Optional[float] = None,
+              cu_seqlens: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+              out_dtype: Optional[torch.dtype] = None, stream: Optional[int] = None) -> torch.Tensor:
+    """softmax(Q K^T * scale) V over [B, H, S, D] views (any batch/head/seq strides, D
+    contiguous).  K/V may carry fewer heads (GQA: query head h reads h / (Hq / Hkv)).
+    ``cu_seqlens`` (int32 [nseg + 1]) adds the block-diagonal segment mask of a packed
+    sequence; ``is_causal`` masks key j > query i.  Default scale 1/sqrt(D); default output dtype
+    is the input dtype."""
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if not t.is_cuda:
+            raise ValueError(f"attention {name} must be a GPU tensor")
+    if not (query.dtype == key.dtype == value.dtype) or query.dtype not in _DTYPE_CODE:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention Q/K/V must share an F32/F16/BF16 dtype")
+    B, Hq, Sq, D = query.shape
+    Bk, Hkv, Skv, Dk = key.shape
+    Bv, Hv, Sv, Dv = value.shape
+    if Bk != B or Bv != B:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention query/key batch mismatch")
+    if Hv != Hkv:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention key/value head mismatch")
+    if Sv != Skv:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention key/value length mismatch")
+    if Dk != D or Dv != D:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention query/key/value width mismatch")
+    odt = out_dtype or (out.dtype if out is not None else query.dtype)
+    if out is None:
+        out = torch.empty((B, Hq, Sq, D), dtype=odt, device=query.device)
+    elif tuple(out.shape) != (B, Hq, Sq, D) or out.dtype != odt:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention out has the wrong shape or dtype")
+    cu_ptr, nseg = None, 0
+    if cu_seqlens is not None:
+        if cu_seqlens.dtype != torch.int32 or not cu_seqlens.is_cuda:
+            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "cu_seqlens must be an int32 GPU tensor")
+        cu_seqlens = cu_seqlens.contiguous()
+        cu_ptr, nseg = cu_seqlens.data_ptr(), cu_seqlens.numel() - 1
+    s = torch.cuda.current_stream(query.device).cuda_stream if stream is None else stream
+    _lib.check(_lib.load().biq_attention(
+        s, query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(),
+        _DTYPE_CODE[query.dtype], _DTYPE_CODE[odt], B, Hq, Hkv, Sq, Skv, D,
+        _strides_bhsd(query, "query"), _strides_bhsd(key, "key"), _strides_bhsd(value, "value"),
+        _strides_bhsd(out, "output"), float(scale) if scale else 0.0, int(bool(is_causal)),
+        cu_ptr, nseg))
+    return out
+
+
+class AttentionKernel:
+    """The reference's kernel seam (attention.rs:47-135), implemented on libbiq.
+
+    ``execute``: Q, K, V [B, H, S, D] -> [B, H, Sq, D].
+    ``execute_gqa``: token-major Q [B, S, Hq, D], K/V [B, S, Hkv, D] -> [B, S, Hq, D]; the
+    head expansion is an index map inside the kernel, never a materialised repeat.
+    The query chunk is validated like the reference's (non-zero) but does not change the result:
+    every query tile of the kernel already sees the complete key/value sequence.
+    """
+
+    SPLIT_DOUBLE_STREAM_SHARED_PROJECTION = False
+
+    @classmethod
+    def execute(cls, query, key, value, query_chunk_size: int, **kw) -> torch.Tensor:
+        if query_chunk_size <= 0:
+            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention query chunk must be non-zero")
+        if key.shape[1] != query.shape[1]:
+            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention query/key head mismatch")
+        return attention(query, key, value, **kw)
+
+    @classmethod
+    def execute_gqa(cls, query, key, value, query_chunk_size: int, **kw) -> torch.Tensor:
+        if query_chunk_size <= 0:
+            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention query chunk must be non-zero")
+        B, S, Hq, D = query.shape
+        _, Sk, Hkv, _ = key.shape
+        if Hq % Hkv != 0:
+            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG,
+                                       "GQA query heads must be divisible by key/value heads")
+        out_dtype = kw.pop("out_dtype", None) or query.dtype
+        out = torch.empty((B, S, Hq, D), dtype=out_dtype, device=query.device)
+        attention(query.permute(0, 2, 1, 3), key.permute(0, 2, 1, 3), value.permute(0, 2, 1, 3),
+                  out=out.permute(0, 2, 1, 3), out_dtype=out_dtype, **kw)
+        return out
+
+
+class NativeQ4FlashAttention(AttentionKernel):
+    """Drop-in for NativeF32ToF16PaddedBlackboxAttention<4, 1, 1> (attention.rs:220-230,406-497):
+    F32 projections in, the HIP flash kernel (f16 matrix-core operands, f32 accumulation), F32 out,
+    with the dual-stream shared projection split (SplitDoubleStreamSharedProjection)."""
+
+    SPLIT_DOUBLE_STREAM_SHARED_PROJECTION = True

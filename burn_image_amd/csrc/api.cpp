@@ -1,0 +1,66 @@
+// C ABI plumbing of libbiq: version, thread-local error state and the Q4S storage contract
+// (host-only helpers that need no GPU).
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "common.h"
+
+namespace biq {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+int fail(int status, const std::string &msg) {
+  g_last_error = msg;
+  return status;
+}
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return fail(BIQ_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+  return BIQ_OK;
+}
+
+}  // namespace biq
+
+extern "C" {
+
+const char *biq_version(void) { return "biq 0.1.0 gfx950"; }
+
+const char *biq_last_error(void) { return biq::g_last_error.c_str(); }
+
+// q4s_storage_block_and_axis (crates/burn_boogu/src/artifacts.rs:513-525).
+int biq_q4_storage_block(int layout, int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  if (layout == BIQ_Q4_NK_AXIS0) return cols % 128 == 0 ? 128 : 0;
+  if (layout == BIQ_Q4_KN_AXIS1) {
+    if (cols % 8 != 0) return 0;
+    static const int groups[5] = {128, 64, 32, 16, 8};
+    for (int g : groups)
+      if (rows % g == 0) return g;
+  }
+  return 0;
+}
+
+// q4s_stored_dtype (artifacts.rs:527-536).
+int biq_q4_stored_dtype(int layout, int64_t rows, int64_t cols, char *buf, size_t buf_len) {
+  biq::clear_error();
+  int block = biq_q4_storage_block(layout, rows, cols);
+  if (block == 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "shape has no exact Q4S storage contract");
+  char tmp[64];
+  if (layout == BIQ_Q4_NK_AXIS0)
+    snprintf(tmp, sizeof tmp, "q4s-block%d-f32-packed-axis0", block);
+  else
+    snprintf(tmp, sizeof tmp, "q4s-block%dx1-f32-packed-axis1", block);
+  if (buf == nullptr || buf_len <= strlen(tmp))
+    return biq::fail(BIQ_ERR_INVALID_ARG, "stored dtype buffer too small");
+  memcpy(buf, tmp, strlen(tmp) + 1);
+  return BIQ_OK;
+}
+
+}  // extern "C"

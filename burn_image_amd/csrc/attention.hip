@@ -1,0 +1,364 @@
+// Exact flash attention for gfx950 (online softmax, LDS-tiled K/V, 64-wide wavefronts).
+//
+// Replaces the forced BlackboxAccelerated cubek kernel (crates/burn_boogu/src/model/
+// native_flash.rs:1006-1090) and Burn's attention op (patches/burn-cubecl-0.21.0/src/ops/
+// module.rs:342-367) for non-causal joint image+text attention, and Qwen's causal / per-segment
+// GQA attention (crates/burn_qwen3_vl/src/text.rs:146-185, vision.rs:344-386).
+//
+// Mapping onto v_mfma_f32_32x32x16_{bf16,f16} (one wave = 32 query rows):
+//  * S^T = K . Q^T: A = a 32-key x 16-d slice of K from LDS, B = Q^T kept in registers.  The
+//    32 x 32 accumulator gives each lane ONE query column (lane & 31) and 16 keys, so the row
+//    max / sum of the online softmax are per-lane register reductions plus one exchange with
+//    lane ^ 32.
+//  * O^T = V^T . P^T: P^T leaves the S^T accumulator already shaped as the B operand (f16).  A
+//    lane's 8 B slots hold keys {0-3, 8-11} (lanes 0-31) or {4-7, 12-15} (lanes 32-63) of each
+//    16-key step, so V is stored transposed in LDS with bits 2 and 3 of the key index swapped;
+//    one 16-byte LDS read then yields the matching A operand.
+//  * Precision: Q K^T in bf16 (bf16 inputs) or f16 (f16/f32 inputs, the reference's F32->F16
+//    bridge), exact products, f32 accumulation; f32 online softmax in base 2; P and V in f16
+//    (u = 2^-11); f32 output accumulation; one final 1/l in f32.
+#include <math.h>
+
+#include <type_traits>
+
+#include "common.h"
+
+namespace {
+
+constexpr int BQ = 128;      // query rows per workgroup (4 waves x 32)
+constexpr int BKV = 64;      // keys per LDS tile
+constexpr int NTHREADS = 256;
+constexpr int VT_LD = BKV + 8;  // halves per row of the transposed V tile
+
+enum MaskMode { MASK_NONE = 0, MASK_CAUSAL = 1, MASK_SEGMENT = 2, MASK_CAUSAL_SEGMENT = 3 };
+
+struct AttnArgs {
+  const void *q, *k, *v;
+  void *o;
+  int64_t qs[3], ks[3], vs[3], os[3];  // batch, head, seq element strides
+  int64_t Hq, Hkv, Sq, Skv, D;
+  float scale_log2;  // softmax scale * log2(e)
+  int out_dtype;
+  const int32_t *cu;
+  int64_t nseg;
+};
+
+// Load 8 consecutive elements of type InT at p and return them as 8 16-bit values of the
+// compute type (bf16 stays bf16 when COMPUTE_BF16, everything else becomes f16).
+template <typename InT, bool COMPUTE_BF16>
+__device__ __forceinline__ u32x4_t load8_compute(const InT *p) {
+  if constexpr (sizeof(InT) == 2) {
+    return *reinterpret_cast<const u32x4_t *>(p);
+  } else {
+    const float4 *f = reinterpret_cast<const float4 *>(p);
+    float4 a = f[0], b = f[1];
+    u32x4_t r;
+    r[0] = biq::pack_f16x2(a.x, a.y);
+    r[1] = biq::pack_f16x2(a.z, a.w);
+    r[2] = biq::pack_f16x2(b.x, b.y);
+    r[3] = biq::pack_f16x2(b.z, b.w);
+    return r;
+  }
+}
+
+// 8 elements of V (InT) -> 8 f16 values (as floats for scattering).
+template <typename InT>
+__device__ __forceinline__ void load8_v_f16(const InT *p, _Float16 out[8]) {
+  if constexpr (sizeof(InT) == 4) {
+    const float4 *f = reinterpret_cast<const float4 *>(p);
+    float4 a = f[0], b = f[1];
+    out[0] = (_Float16)a.x; out[1] = (_Float16)a.y; out[2] = (_Float16)a.z; out[3] = (_Float16)a.w;
+    out[4] = (_Float16)b.x; out[5] = (_Float16)b.y; out[6] = (_Float16)b.z; out[7] = (_Float16)b.w;
+  } else if constexpr (std::is_same<InT, bf16_t>::value) {
+    u32x4_t v = *reinterpret_cast<const u32x4_t *>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = (_Float16)biq::bf16_lo_to_f32(v[i]);
+      out[2 * i + 1] = (_Float16)biq::bf16_hi_to_f32(v[i]);
+    }
+  } else {
+    u32x4_t v = *reinterpret_cast<const u32x4_t *>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = biq::bitcast<_Float16>((uint16_t)(v[i] & 0xffffu));
+      out[2 * i + 1] = biq::bitcast<_Float16>((uint16_t)(v[i] >> 16));
+    }
+  }
+}
+
+// Physical position of key c inside its 16-key group of the transposed V tile (swap bits 2, 3).
+__device__ __forceinline__ int vt_slot(int key) {
+  return (key & ~15) | (key & 3) | ((key & 4) << 1) | ((key & 8) >> 1);
+}
+
+__device__ __forceinline__ int64_t segment_of(const int32_t *cu, int64_t nseg, int64_t i) {
+  int64_t lo = 0, hi = nseg - 1;
+  while (lo < hi) {
+    int64_t mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= i) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+template <int DP, typename InT, int MASK>
+__global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
+  constexpr bool BF16 = std::is_same<InT, bf16_t>::value;
+  constexpr int KS_LD = DP + 8;  // halves per row of the K tile
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[BKV * KS_LD];
+  __shared__ __attribute__((aligned(16))) _Float16 Vt[DP * VT_LD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const int64_t hk = h / (p.Hq / p.Hkv);
+  const int64_t qblk = (int64_t)blockIdx.x * BQ;
+  const int64_t qi = qblk + wave * 32 + l32;  // this lane's query row
+  const int64_t D = p.D;
+
+  const InT *qg = reinterpret_cast<const InT *>(p.q) + b * p.qs[0] + h * p.qs[1];
+  const InT *kg = reinterpret_cast<const InT *>(p.k) + b * p.ks[0] + hk * p.ks[1];
+  const InT *vg = reinterpret_cast<const InT *>(p.v) + b * p.vs[0] + hk * p.vs[1];
+
+  // ---- Q^T fragments (B operand of S^T = K Q^T): lane holds d = 16 s + 8 lh .. +7 of row qi
+  u32x4_t qf[DP / 16];
+#pragma unroll
+  for (int s = 0; s < DP / 16; ++s) {
+    const int d0 = 16 * s + 8 * lh;
+    if (qi < p.Sq && d0 < D)
+      qf[s] = load8_compute<InT, BF16>(qg + qi * p.qs[2] + d0);
+    else
+      qf[s] = u32x4_t{0u, 0u, 0u, 0u};
+  }
+
+  // ---- key range of this workgroup and visibility bounds of this lane's query
+  int64_t kv_begin = 0, kv_end = p.Skv;
+  int64_t seg_lo = 0, seg_hi = p.Skv;
+  if constexpr (MASK & MASK_SEGMENT) {
+    const int64_t qc = qi < p.Sq ? qi : p.Sq - 1;
+    const int64_t sg = segment_of(p.cu, p.nseg, qc);
+    seg_lo = p.cu[sg];
+    seg_hi = p.cu[sg + 1];
+    const int64_t qlast = (qblk + BQ - 1) < p.Sq ? (qblk + BQ - 1) : p.Sq - 1;
+    kv_begin = p.cu[segment_of(p.cu, p.nseg, qblk)];
+    kv_end = p.cu[segment_of(p.cu, p.nseg, qlast) + 1];
+  }
+  if constexpr (MASK & MASK_CAUSAL) {
+    const int64_t qlast = (qblk + BQ - 1) < p.Sq ? (qblk + BQ - 1) : p.Sq - 1;
+    kv_end = kv_end < qlast + 1 ? kv_end : qlast + 1;
+  }
+  kv_begin = (kv_begin / BKV) * BKV;
+
+  floatx16_t oacc[DP / 32];
+#pragma unroll
+  for (int i = 0; i < DP / 32; ++i) oacc[i] = biq::zero16();
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  for (int64_t kv0 = kv_begin; kv0 < kv_end; kv0 += BKV) {
+    __syncthreads();
+    // ---- stage K (compute type, row-major) and V (f16, transposed + slot-permuted)
+#pragma unroll
+    for (int it = 0; it < (BKV * DP / 8) / NTHREADS; ++it) {
+      const int c = tid + it * NTHREADS;
+      const int row = c / (DP / 8), ch = c % (DP / 8);
+      const int64_t key = kv0 + row;
+      const int d0 = 8 * ch;
+      u32x4_t kv = {0u, 0u, 0u, 0u};
+      _Float16 vv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (key < p.Skv && d0 < D) {
+        kv = load8_compute<InT, BF16>(kg + key * p.ks[2] + d0);
+        load8_v_f16<InT>(vg + key * p.vs[2] + d0, vv);
+      }
+      *reinterpret_cast<u32x4_t *>(&Ks[row * KS_LD + d0]) = kv;
+      const int slot = vt_slot(row);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Vt[(d0 + e) * VT_LD + slot] = vv[e];
+    }
+    __syncthreads();
+
+    // ---- S^T = K Q^T for the tile's 64 keys (2 x 32)
+    floatx16_t sacc[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      floatx16_t a = biq::zero16();
+#pragma unroll
+      for (int s = 0; s < DP / 16; ++s) {
+        const u32x4_t kf =
+            *reinterpret_cast<const u32x4_t *>(&Ks[(32 * ks + l32) * KS_LD + 16 * s + 8 * lh]);
+        if constexpr (BF16)
+          a = biq::mfma32x32x16_bf16(biq::bitcast<bf16x8_t>(kf), biq::bitcast<bf16x8_t>(qf[s]), a);
+        else
+          a = biq::mfma32x32x16_f16(biq::bitcast<half8_t>(kf), biq::bitcast<half8_t>(qf[s]), a);
+      }
+      sacc[ks] = a;
+    }
+
+    // ---- scale, mask, online softmax (base 2)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t key = kv0 + 32 * ks + 8 * (r >> 2) + 4 * lh + (r & 3);
+        bool ok = key < p.Skv;
+        if constexpr (MASK & MASK_SEGMENT) ok = ok && key >= seg_lo && key < seg_hi;
+        if constexpr (MASK & MASK_CAUSAL) ok = ok && key <= qi;
+        const float x = ok ? sacc[ks][r] * p.scale_log2 : -INFINITY;
+        sacc[ks][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    float rs = 0.0f;
+    u32x4_t pf[4];  // P^T as f16 B operands of the four 16-key steps
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e0 = __builtin_amdgcn_exp2f(sacc[ks][8 * t + 2 * j] - m_use);
+          const float e1 = __builtin_amdgcn_exp2f(sacc[ks][8 * t + 2 * j + 1] - m_use);
+          rs += e0 + e1;
+          pf[2 * ks + t][j] = biq::pack_f16x2(e0, e1);
+        }
+    l_run = l_run * alpha + rs;
+#pragma unroll
+    for (int i = 0; i < DP / 32; ++i) oacc[i] *= alpha;
+
+    // ---- O^T += V^T P^T
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const half8_t bp = biq::bitcast<half8_t>(pf[t]);
+#pragma unroll
+      for (int i = 0; i < DP / 32; ++i) {
+        const half8_t av =
+            *reinterpret_cast<const half8_t *>(&Vt[(32 * i + l32) * VT_LD + 16 * t + 8 * lh]);
+        oacc[i] = biq::mfma32x32x16_f16(av, bp, oacc[i]);
+      }
+    }
+  }
+
+  // ---- normalise and store O[b, h, qi, d]
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (qi >= p.Sq) return;
+  char *ob = reinterpret_cast<char *>(p.o);
+  const int64_t obase = b * p.os[0] + h * p.os[1] + qi * p.os[2];
+#pragma unroll
+  for (int i = 0; i < DP / 32; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 32 * i + 8 * g + 4 * lh;
+      if (d0 >= D) continue;
+      const float v0 = oacc[i][4 * g] * inv, v1 = oacc[i][4 * g + 1] * inv;
+      const float v2 = oacc[i][4 * g + 2] * inv, v3 = oacc[i][4 * g + 3] * inv;
+      if (p.out_dtype == BIQ_DTYPE_F32) {
+        float *dst = reinterpret_cast<float *>(ob) + obase + d0;
+        *reinterpret_cast<float4 *>(dst) = make_float4(v0, v1, v2, v3);
+      } else if (p.out_dtype == BIQ_DTYPE_F16) {
+        uint16_t *dst = reinterpret_cast<uint16_t *>(ob) + obase + d0;
+        uint2 w = make_uint2(biq::pack_f16x2(v0, v1), biq::pack_f16x2(v2, v3));
+        *reinterpret_cast<uint2 *>(dst) = w;
+      } else {
+        uint16_t *dst = reinterpret_cast<uint16_t *>(ob) + obase + d0;
+        uint2 w = make_uint2(biq::f32_to_bf16_bits(v0) | (biq::f32_to_bf16_bits(v1) << 16),
+                             biq::f32_to_bf16_bits(v2) | (biq::f32_to_bf16_bits(v3) << 16));
+        *reinterpret_cast<uint2 *>(dst) = w;
+      }
+    }
+}
+
+template <int DP, typename InT>
+void launch_mask(hipStream_t s, dim3 grid, const AttnArgs &a, int mask) {
+  switch (mask) {
+    case MASK_NONE:
+      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_NONE>), grid, dim3(NTHREADS), 0, s, a);
+      break;
+    case MASK_CAUSAL:
+      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_CAUSAL>), grid, dim3(NTHREADS), 0, s, a);
+      break;
+    case MASK_SEGMENT:
+      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_SEGMENT>), grid, dim3(NTHREADS), 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_CAUSAL_SEGMENT>), grid, dim3(NTHREADS), 0,
+                         s, a);
+      break;
+  }
+}
+
+template <int DP>
+void launch_dtype(hipStream_t s, dim3 grid, const AttnArgs &a, int in_dtype, int mask) {
+  if (in_dtype == BIQ_DTYPE_BF16) launch_mask<DP, bf16_t>(s, grid, a, mask);
+  else if (in_dtype == BIQ_DTYPE_F16) launch_mask<DP, f16_t>(s, grid, a, mask);
+  else launch_mask<DP, float>(s, grid, a, mask);
+}
+
+}  // namespace
+
+extern "C" int biq_attention(void *stream, const void *q, const void *k, const void *v, void *o,
+                             int in_dtype, int out_dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                             int64_t Sq, int64_t Skv, int64_t D, const int64_t *q_strides,
+                             const int64_t *k_strides, const int64_t *v_strides,
+                             const int64_t *o_strides, float scale, int causal,
+                             const int32_t *cu_seqlens, int64_t nseg) {
+  biq::clear_error();
+  if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "null pointer argument");
+  if (in_dtype != BIQ_DTYPE_F32 && in_dtype != BIQ_DTYPE_F16 && in_dtype != BIQ_DTYPE_BF16)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "attention input dtype must be F32, F16 or BF16");
+  if (out_dtype != BIQ_DTYPE_F32 && out_dtype != BIQ_DTYPE_F16 && out_dtype != BIQ_DTYPE_BF16)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "attention output dtype must be F32, F16 or BF16");
+  if (B <= 0 || Hq <= 0 || Hkv <= 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "attention batch and heads must be non-zero");
+  if (Sq <= 0) return biq::fail(BIQ_ERR_INVALID_ARG, "attention query sequence must be non-empty");
+  if (Skv <= 0) return biq::fail(BIQ_ERR_INVALID_ARG, "attention key sequence must be non-empty");
+  if (Hq % Hkv != 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "GQA query heads must be divisible by key/value heads");
+  if (D <= 0 || D > 128 || D % 8 != 0)
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "attention head width must be a multiple of 8 up to 128");
+  if ((causal || cu_seqlens) && Sq != Skv)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "causal and segment masks require Sq == Skv");
+  if (cu_seqlens && nseg <= 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "segment mask requires at least one segment");
+  const int esz = in_dtype == BIQ_DTYPE_F32 ? 4 : 2;
+  const int osz = out_dtype == BIQ_DTYPE_F32 ? 4 : 2;
+  const int64_t *st[3] = {q_strides, k_strides, v_strides};
+  const void *ptr[3] = {q, k, v};
+  for (int t = 0; t < 3; ++t) {
+    if (reinterpret_cast<uintptr_t>(ptr[t]) & 15)
+      return biq::fail(BIQ_ERR_INVALID_ARG, "attention inputs must be 16-byte aligned");
+    for (int j = 0; j < 3; ++j)
+      if (((st[t][j] * esz) & 15) != 0)
+        return biq::fail(BIQ_ERR_INVALID_ARG, "attention strides must be multiples of 16 bytes");
+  }
+  if (reinterpret_cast<uintptr_t>(o) & 15)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "attention output must be 16-byte aligned");
+  for (int j = 0; j < 3; ++j)
+    if (((o_strides[j] * osz) & 15) != 0)
+      return biq::fail(BIQ_ERR_INVALID_ARG, "attention output strides must be multiples of 16 bytes");
+  if (B > 65535 || Hq > 65535 || (Sq + BQ - 1) / BQ > 0x7fffffff)
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "attention grid too large");
+
+  AttnArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o;
+  for (int j = 0; j < 3; ++j) {
+    a.qs[j] = q_strides[j]; a.ks[j] = k_strides[j]; a.vs[j] = v_strides[j]; a.os[j] = o_strides[j];
+  }
+  a.Hq = Hq; a.Hkv = Hkv; a.Sq = Sq; a.Skv = Skv; a.D = D;
+  const double sc = scale > 0.0f ? (double)scale : 1.0 / sqrt((double)D);
+  a.scale_log2 = (float)(sc * 1.4426950408889634);
+  a.out_dtype = out_dtype;
+  a.cu = cu_seqlens;
+  a.nseg = nseg;
+  const int mask = (causal ? MASK_CAUSAL : 0) | (cu_seqlens ? MASK_SEGMENT : 0);
+  dim3 grid((unsigned)((Sq + BQ - 1) / BQ), (unsigned)Hq, (unsigned)B);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (D <= 64) launch_dtype<64>(s, grid, a, in_dtype, mask);
+  else launch_dtype<128>(s, grid, a, in_dtype, mask);
+  return biq::check_launch("attention");
+}

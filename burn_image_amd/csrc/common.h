@@ -1,0 +1,79 @@
+// Shared helpers for the gfx950 kernels of libbiq: vector types, 16-bit conversions, MFMA
+// wrappers and the thread-local error state of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/biq.h"
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw 16-bit element tags used as kernel template parameters.
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+namespace biq {
+
+// ---------------------------------------------------------------------------------------------
+// error state (host)
+// ---------------------------------------------------------------------------------------------
+void set_error(const std::string &msg);
+void clear_error();
+int fail(int status, const std::string &msg);
+// Check the launch status of the last kernel on this thread.
+int check_launch(const char *what);
+
+// ---------------------------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------------------------
+template <typename T, typename F>
+__device__ __forceinline__ T bitcast(const F &f) {
+  static_assert(sizeof(T) == sizeof(F), "bitcast size");
+  return __builtin_bit_cast(T, f);
+}
+
+__device__ __forceinline__ float bf16_lo_to_f32(uint32_t d) { return bitcast<float>(d << 16); }
+__device__ __forceinline__ float bf16_hi_to_f32(uint32_t d) { return bitcast<float>(d & 0xffff0000u); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return (float)bitcast<_Float16>(h);
+}
+
+// Round-to-nearest-even f32 -> bf16 bits (finite inputs; NaN stays NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = bitcast<uint32_t>(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  half2_t h = {(_Float16)lo, (_Float16)hi};
+  return bitcast<uint32_t>(h);
+}
+
+__device__ __forceinline__ floatx16_t mfma32x32x16_f16(const half8_t &a, const half8_t &b,
+                                                       const floatx16_t &c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx16_t mfma32x32x16_bf16(const bf16x8_t &a, const bf16x8_t &b,
+                                                        const floatx16_t &c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx16_t zero16() {
+  floatx16_t z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+}  // namespace biq

@@ -1,0 +1,357 @@
+// Packed signed-Q4 projection GEMM for gfx950: y[M, N] = x[M, K] . W (+ bias).
+//
+// Replaces the quantized CMMA matmul behind QTensorOps::q_matmul
+// (patches/burn-cubecl-0.21.0/src/ops/qtensor.rs:303-368, kernel/matmul/quantized.rs:35-60).
+//
+// Arithmetic (exact where it matters for the f32-result parity gate):
+//  * Each packed word holds 8 consecutive k of one column n.  A lane of v_mfma_f32_32x32x16_f16's
+//    B operand holds exactly 8 consecutive k of one column, so one word feeds one lane-operand.
+//  * Nibbles decode to EXACT f16 integers: (0x6400 | (v ^ 8)) is 1024 + q + 8 in f16, and one
+//    v_pk_add_f16 of -1032 leaves q in [-8, 7].  The word is split as (k0,k4),(k1,k5),(k2,k6),
+//    (k3,k7) pairs, so B slots carry k in the order [0,4,1,5,2,6,3,7]; the activations are written
+//    to LDS in the same order, which leaves every product x[k] * q[k] paired correctly.
+//  * Activations enter as f16: bf16 -> f16 is exact for |x| >= 2^-14 (the reference itself stages
+//    f16, kernel/matmul/quantized.rs:172-178); f32 activations are split into f16 hi + lo
+//    (x - hi rounded again), two MFMAs, leaving a 2^-22 relative residual.
+//  * Products are exact in the f32 accumulator.  Each K-block's partial sum is kept in its own
+//    accumulator and added to the output accumulator as acc += scale[b, n] * partial in f32,
+//    so the f32 block scale is never rounded to 16 bits.
+//
+// Tiling: 256 threads = 4 waves in a 2 x 2 grid, workgroup tile 128 x 128, wave tile 64 x 64
+// (2 x 2 MFMA 32 x 32 tiles), K staged 64 at a time through LDS.
+#include "common.h"
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 64, NTHREADS = 256;
+constexpr int A_LD = BK + 8;  // LDS row stride of the activation tile, in halves (16 B pad)
+constexpr int B_LD = BN;      // LDS row stride of the word tile, in words
+
+enum XMode { XM_F16 = 0, XM_BF16 = 1, XM_F32 = 2 };
+
+// Eight signed nibbles -> eight exact f16 integers in slot order [k0,k4,k1,k5,k2,k6,k3,k7].
+__device__ __forceinline__ half8_t unpack_q4_f16(uint32_t w) {
+  const uint32_t M = 0x000F000Fu;  // nibbles i and i + 4 of the shifted word
+  const uint32_t C = 0x64086408u;  // f16 1024.0 exponent pattern | sign-flip bit of the nibble
+  u32x4_t d;
+  d[0] = ((w ^ C) & M) | (C & ~M);
+  d[1] = (((w >> 4) ^ C) & M) | (C & ~M);
+  d[2] = (((w >> 8) ^ C) & M) | (C & ~M);
+  d[3] = (((w >> 12) ^ C) & M) | (C & ~M);
+  half8_t h = biq::bitcast<half8_t>(d);
+  const _Float16 off = (_Float16)(-1032.0f);
+  return h + off;
+}
+
+// 8 bf16 -> 8 f16 in slot order [0,4,1,5,2,6,3,7].
+__device__ __forceinline__ u32x4_t bf16x8_to_f16_slots(u32x4_t v) {
+  u32x4_t r;
+  r[0] = biq::pack_f16x2(biq::bf16_lo_to_f32(v[0]), biq::bf16_lo_to_f32(v[2]));
+  r[1] = biq::pack_f16x2(biq::bf16_hi_to_f32(v[0]), biq::bf16_hi_to_f32(v[2]));
+  r[2] = biq::pack_f16x2(biq::bf16_lo_to_f32(v[1]), biq::bf16_lo_to_f32(v[3]));
+  r[3] = biq::pack_f16x2(biq::bf16_hi_to_f32(v[1]), biq::bf16_hi_to_f32(v[3]));
+  return r;
+}
+
+// 8 f16 -> slot order [0,4,1,5,2,6,3,7].
+__device__ __forceinline__ u32x4_t f16x8_to_slots(u32x4_t v) {
+  u32x4_t r;
+  r[0] = (v[0] & 0xffffu) | (v[2] << 16);
+  r[1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
+  r[2] = (v[1] & 0xffffu) | (v[3] << 16);
+  r[3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
+  return r;
+}
+
+// 8 f32 -> (hi, lo) f16 slots, x = hi + lo to within 2^-22 relative.
+__device__ __forceinline__ void f32x8_to_f16_split_slots(const float4 &a, const float4 &b,
+                                                         u32x4_t &hi, u32x4_t &lo) {
+  float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  _Float16 h[8];
+  float l[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    h[i] = (_Float16)x[i];
+    l[i] = x[i] - (float)h[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    half2_t hh = {h[i], h[i + 4]};
+    hi[i] = biq::bitcast<uint32_t>(hh);
+    lo[i] = biq::pack_f16x2(l[i], l[i + 4]);
+  }
+}
+
+template <int LAYOUT>
+__device__ __forceinline__ float load_scale(const float *__restrict__ scales, int64_t b, int64_t n,
+                                            int64_t N, int64_t nblk) {
+  if (n >= N || b >= nblk) return 0.0f;
+  return LAYOUT == BIQ_Q4_KN_AXIS1 ? scales[b * N + n] : scales[n * nblk + b];
+}
+
+template <int LAYOUT, int XMODE, int BLK>
+__global__ void __launch_bounds__(NTHREADS, 1)
+    q4_gemm_kernel(const void *__restrict__ xv, int64_t ldx, const uint32_t *__restrict__ words,
+                   const float *__restrict__ scales, const float *__restrict__ bias,
+                   void *__restrict__ yv, int y_dtype, int64_t M, int64_t N, int64_t K) {
+  constexpr int NSPLIT = XMODE == XM_F32 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) uint16_t As[NSPLIT][BM * A_LD];
+  __shared__ __attribute__((aligned(16))) uint32_t Bs[(BK / 8) * B_LD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+  const int64_t nblk = K / BLK;
+  const int64_t KW = K / 8;
+
+  floatx16_t acc[2][2], part[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      acc[i][j] = biq::zero16();
+      part[i][j] = biq::zero16();
+    }
+
+  int64_t ncol[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) ncol[j] = n0 + wn * 64 + 32 * j + l32;
+
+  for (int64_t kt = 0; kt < K; kt += BK) {
+    // ---------------- stage the activation tile (BM x BK) into LDS as f16 slots -------------
+#pragma unroll
+    for (int it = 0; it < (BM * BK / 8) / NTHREADS; ++it) {
+      const int c = tid + it * NTHREADS;
+      const int row = c >> 3, kc = c & 7;
+      const int64_t gm = m0 + row, gk = kt + 8 * kc;
+      u32x4_t hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
+      if (gm < M && gk < K) {
+        if constexpr (XMODE == XM_BF16) {
+          const u32x4_t v = *reinterpret_cast<const u32x4_t *>(
+              reinterpret_cast<const uint16_t *>(xv) + gm * ldx + gk);
+          hi = bf16x8_to_f16_slots(v);
+        } else if constexpr (XMODE == XM_F16) {
+          const u32x4_t v = *reinterpret_cast<const u32x4_t *>(
+              reinterpret_cast<const uint16_t *>(xv) + gm * ldx + gk);
+          hi = f16x8_to_slots(v);
+        } else {
+          const float4 *src =
+              reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(xv) + gm * ldx + gk);
+          f32x8_to_f16_split_slots(src[0], src[1], hi, lo);
+        }
+      }
+      *reinterpret_cast<u32x4_t *>(&As[0][row * A_LD + 8 * kc]) = hi;
+      if constexpr (NSPLIT == 2) *reinterpret_cast<u32x4_t *>(&As[1][row * A_LD + 8 * kc]) = lo;
+    }
+    // ---------------- stage the packed word tile (BK/8 x BN words) into LDS -----------------
+    {
+      const int64_t kw0 = kt / 8;
+      if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
+        const int kwr = tid >> 5, nc = (tid & 31) * 4;
+        u32x4_t w = {0u, 0u, 0u, 0u};
+        if (kw0 + kwr < KW && n0 + nc < N)
+          w = *reinterpret_cast<const u32x4_t *>(words + (kw0 + kwr) * N + n0 + nc);
+        *reinterpret_cast<u32x4_t *>(&Bs[kwr * B_LD + nc]) = w;
+      } else {
+        const int nl = tid >> 1, half = tid & 1;
+        const int64_t n = n0 + nl;
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        if (n < N) {
+          const int64_t kwb = kw0 + 4 * half;
+          const uint32_t *src = words + n * KW + kwb;
+          if ((KW & 3) == 0 && kwb + 3 < KW) {
+            const u32x4_t v = *reinterpret_cast<const u32x4_t *>(src);
+            w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (kwb + j < KW) w[j] = src[j];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Bs[(4 * half + j) * B_LD + nl] = w[j];
+      }
+    }
+    // per-tile scales: every block that ends inside this tile
+    constexpr int TILE_BLOCKS = BLK >= BK ? 1 : BK / BLK;
+    constexpr int SCALES_PER_TILE = BLK == 8 ? TILE_BLOCKS : TILE_BLOCKS;
+    float sc[2][SCALES_PER_TILE];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int t = 0; t < SCALES_PER_TILE; ++t)
+        sc[j][t] = load_scale<LAYOUT>(scales, kt / BLK + t, ncol[j], N, nblk);
+
+    __syncthreads();
+
+    // ---------------- MFMA over the 4 K16 steps of the tile --------------------------------
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      if (kt + 16 * s >= K) break;
+      half8_t a[2][NSPLIT];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int x = 0; x < NSPLIT; ++x)
+          a[i][x] = *reinterpret_cast<const half8_t *>(
+              &As[x][(wm * 64 + 32 * i + l32) * A_LD + 16 * s + 8 * lh]);
+      half8_t bq[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bq[j] = unpack_q4_f16(Bs[(2 * s + lh) * B_LD + wn * 64 + 32 * j + l32]);
+
+      if constexpr (BLK == 8) {
+        // Lanes 0-31 carry block 2g, lanes 32-63 block 2g + 1: two masked MFMAs per tile.
+        const half8_t zh = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const half8_t b_lo = lh == 0 ? bq[j] : zh;
+          const half8_t b_hi = lh == 0 ? zh : bq[j];
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            floatx16_t p = biq::mfma32x32x16_f16(a[i][0], b_lo, biq::zero16());
+            if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a[i][1], b_lo, p);
+            acc[i][j] += sc[j][2 * s] * p;
+            p = biq::mfma32x32x16_f16(a[i][0], b_hi, biq::zero16());
+            if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a[i][1], b_hi, p);
+            acc[i][j] += sc[j][2 * s + 1] * p;
+          }
+        }
+      } else {
+        constexpr int SPB = BLK / 16;  // K16 steps per block
+        bool first, last;
+        int tb;  // index of this step's block within the tile's scale list
+        if constexpr (BLK >= BK) {
+          first = (s == 0) && (kt % BLK == 0);
+          last = (s == BK / 16 - 1) && ((kt + BK) % BLK == 0);
+          tb = 0;
+        } else {
+          first = (s % SPB) == 0;
+          last = (s % SPB) == SPB - 1;
+          tb = s / SPB;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            floatx16_t p = first ? biq::zero16() : part[i][j];
+            p = biq::mfma32x32x16_f16(a[i][0], bq[j], p);
+            if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a[i][1], bq[j], p);
+            part[i][j] = p;
+          }
+        if (last) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] += sc[j][tb] * part[i][j];
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---------------- epilogue: bias, convert, store ------------------------------------------
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t col = ncol[j];
+    if (col >= N) continue;
+    const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (row >= M) continue;
+        const float v = acc[i][j][r] + bv;
+        if (y_dtype == BIQ_DTYPE_F32) {
+          reinterpret_cast<float *>(yv)[row * N + col] = v;
+        } else if (y_dtype == BIQ_DTYPE_F16) {
+          reinterpret_cast<_Float16 *>(yv)[row * N + col] = (_Float16)v;
+        } else {
+          reinterpret_cast<uint16_t *>(yv)[row * N + col] = (uint16_t)biq::f32_to_bf16_bits(v);
+        }
+      }
+  }
+}
+
+template <int LAYOUT, int XMODE>
+int launch_blk(hipStream_t s, int block, const void *x, int64_t ldx, const uint32_t *words,
+               const float *scales, const float *bias, void *y, int y_dtype, int64_t M, int64_t N,
+               int64_t K) {
+  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+  dim3 blk(NTHREADS);
+  switch (block) {
+    case 8:
+      hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, 8>), grid, blk, 0, s, x, ldx, words,
+                         scales, bias, y, y_dtype, M, N, K);
+      break;
+    case 16:
+      hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, 16>), grid, blk, 0, s, x, ldx, words,
+                         scales, bias, y, y_dtype, M, N, K);
+      break;
+    case 32:
+      hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, 32>), grid, blk, 0, s, x, ldx, words,
+                         scales, bias, y, y_dtype, M, N, K);
+      break;
+    case 64:
+      hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, 64>), grid, blk, 0, s, x, ldx, words,
+                         scales, bias, y, y_dtype, M, N, K);
+      break;
+    default:
+      hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, 128>), grid, blk, 0, s, x, ldx, words,
+                         scales, bias, y, y_dtype, M, N, K);
+      break;
+  }
+  return biq::check_launch("q4 linear");
+}
+
+template <int LAYOUT>
+int launch_layout(hipStream_t s, int x_dtype, int block, const void *x, int64_t ldx,
+                  const uint32_t *words, const float *scales, const float *bias, void *y,
+                  int y_dtype, int64_t M, int64_t N, int64_t K) {
+  switch (x_dtype) {
+    case BIQ_DTYPE_BF16:
+      return launch_blk<LAYOUT, XM_BF16>(s, block, x, ldx, words, scales, bias, y, y_dtype, M, N, K);
+    case BIQ_DTYPE_F16:
+      return launch_blk<LAYOUT, XM_F16>(s, block, x, ldx, words, scales, bias, y, y_dtype, M, N, K);
+    default:
+      return launch_blk<LAYOUT, XM_F32>(s, block, x, ldx, words, scales, bias, y, y_dtype, M, N, K);
+  }
+}
+
+}  // namespace
+
+extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K,
+                             int64_t ldx, const uint32_t *words, const float *scales, int layout,
+                             int block, int64_t N, const float *bias, void *y, int y_dtype) {
+  biq::clear_error();
+  if (!x || !words || !scales || !y) return biq::fail(BIQ_ERR_INVALID_ARG, "null pointer argument");
+  if (layout != BIQ_Q4_KN_AXIS1 && layout != BIQ_Q4_NK_AXIS0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "unknown Q4 layout");
+  if (x_dtype != BIQ_DTYPE_F32 && x_dtype != BIQ_DTYPE_F16 && x_dtype != BIQ_DTYPE_BF16)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "activation dtype must be F32, F16 or BF16");
+  if (y_dtype != BIQ_DTYPE_F32 && y_dtype != BIQ_DTYPE_F16 && y_dtype != BIQ_DTYPE_BF16)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "output dtype must be F32, F16 or BF16");
+  if (block != 8 && block != 16 && block != 32 && block != 64 && block != 128)
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "Q4 block must be one of 8, 16, 32, 64, 128");
+  if (M <= 0 || N <= 0 || K <= 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "q4 linear requires non-empty M, N and K");
+  if (K % 8 != 0 || K % block != 0 || N % 8 != 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "q4 linear requires K % 8 == 0, K % block == 0, N % 8 == 0");
+  if (ldx < K) return biq::fail(BIQ_ERR_INVALID_ARG, "activation row stride is smaller than K");
+  const int esz = x_dtype == BIQ_DTYPE_F32 ? 4 : 2;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || ((ldx * esz) & 15) ||
+      (reinterpret_cast<uintptr_t>(words) & 15) || (reinterpret_cast<uintptr_t>(scales) & 3))
+    return biq::fail(BIQ_ERR_INVALID_ARG,
+                     "q4 linear requires 16-byte aligned activation rows and packed words");
+  if (M > (int64_t)65535 * 128)
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "q4 linear supports at most 8388480 rows per call");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (layout == BIQ_Q4_KN_AXIS1)
+    return launch_layout<BIQ_Q4_KN_AXIS1>(s, x_dtype, block, x, ldx, words, scales, bias, y, y_dtype,
+                                          M, N, K);
+  return launch_layout<BIQ_Q4_NK_AXIS0>(s, x_dtype, block, x, ldx, words, scales, bias, y, y_dtype,
+                                        M, N, K);
+}

@@ -1,0 +1,125 @@
+/*
+ * biq.h - C ABI of the MI355X (gfx950) denoiser attention block library (libbiq.so).
+ *
+ * The library replaces the Burn/CubeCL operators below burn_boogu's attention and linear seams
+ * with hand-written HIP kernels: packed signed-Q4 projection GEMMs (f32 block scales), Q4S
+ * quantisation / dequantisation, and exact flash attention (non-causal, causal, segment-masked,
+ * GQA).  Every entry point:
+ *   - takes plain device pointers, element counts and an optional HIP stream (`stream` is a
+ *     hipStream_t; NULL selects the default stream) and is asynchronous on that stream unless
+ *     stated otherwise;
+ *   - returns BIQ_OK or an error status and never falls back to another implementation; the
+ *     message of the last failure on the calling thread is available from biq_last_error();
+ *   - never frees caller memory; the caller owns every input and output buffer.
+ * Calls are reentrant and thread-safe.  Reference citations are file:line in mosure/burn_image.
+ */
+#ifndef BIQ_H
+#define BIQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  INVALID_ARG mirrors the reference's fail-closed shape/dtype/divisibility asserts
+ * (crates/burn_boogu/src/model/native_flash.rs:1713-1727,1913-1955; attention.rs:78-90) and the
+ * quantizers' `Err` results (crates/burn_boogu/src/artifacts.rs:7213-7236,7306-7340). */
+#define BIQ_OK 0
+#define BIQ_ERR_INVALID_ARG 1
+#define BIQ_ERR_UNSUPPORTED 2
+#define BIQ_ERR_HIP 3
+
+/* Element types of activations and outputs. */
+#define BIQ_DTYPE_F32 0
+#define BIQ_DTYPE_F16 1
+#define BIQ_DTYPE_BF16 2
+
+/* Packed signed-Q4 layouts (eight signed nibbles per little-endian u32, lane l at bits 4l..4l+3).
+ * BIQ_Q4_NK_AXIS0: Qwen `PackedU32(0)`, block [blk]: weight [N, K] (checkpoint [out, in]); words
+ *   [N, K/8], scales f32 [N, K/blk]; the GEMM consumes W^T (artifacts.rs:7203-7288,518;
+ *   crates/burn_qwen3_vl/src/linear.rs:58-62).
+ * BIQ_Q4_KN_AXIS1: Boogu `PackedU32(1)`, block [blk, 1]: weight [K, N] ([input, output]); words
+ *   [K/8, N], word (kw, n) holds k = 8*kw + l; scales f32 [K/blk, N] (artifacts.rs:7296-7388). */
+#define BIQ_Q4_NK_AXIS0 0
+#define BIQ_Q4_KN_AXIS1 1
+
+/* Library version string, e.g. "biq 0.1.0 gfx950". */
+const char *biq_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *biq_last_error(void);
+
+/* Storage block of a Q4S weight of logical shape [rows, cols] for `layout`, or 0 if the
+ * reference would not store it as Q4S.  Replaces q4s_storage_block_and_axis
+ * (crates/burn_boogu/src/artifacts.rs:513-525): Qwen ([N, K], layout 0) needs K % 128 == 0 and
+ * uses 128; Boogu ([K, N], layout 1) needs N % 8 == 0 and uses the largest of 128, 64, 32, 16, 8
+ * dividing K.  Host-only; no GPU needed. */
+int biq_q4_storage_block(int layout, int64_t rows, int64_t cols);
+
+/* Tensor-inventory dtype string of that storage contract, written to buf (NUL-terminated):
+ * "q4s-block{b}-f32-packed-axis0" or "q4s-block{b}x1-f32-packed-axis1" (artifacts.rs:527-536).
+ * Returns BIQ_ERR_INVALID_ARG if the shape has no Q4S contract or buf is too small. Host-only. */
+int biq_q4_stored_dtype(int layout, int64_t rows, int64_t cols, char *buf, size_t buf_len);
+
+/* Quantise an f32 weight on the GPU, byte-for-byte as the reference importer does.
+ * layout BIQ_Q4_KN_AXIS1: w is [K, N] -> quantize_row_layout_q4s_block_up_to128_f32
+ *   (artifacts.rs:7296-7388), block = biq_q4_storage_block(1, K, N).
+ * layout BIQ_Q4_NK_AXIS0: w is [N, K] -> quantize_q4s_block128_f32 (artifacts.rs:7203-7288),
+ *   block 128 along K.
+ * words/scales receive the layout's buffers.  Synchronous: it waits for the stream so that a
+ * non-finite input can be reported as BIQ_ERR_INVALID_ARG, as the reference returns Err. */
+int biq_q4_quantize(void *stream, const float *w, int layout, int64_t K, int64_t N,
+                    uint32_t *words, float *scales);
+
+/* Dequantise to f32, bit-exact `f32(q) * scale` (artifacts.rs:10434-10440; the GPU dequant
+ * call patches/burn-cubecl-0.21.0/src/kernel/quantization/dequantize.rs:6-34).  Output is the
+ * tensor's logical shape: [K, N] for BIQ_Q4_KN_AXIS1, [N, K] for BIQ_Q4_NK_AXIS0. */
+int biq_q4_dequant_f32(void *stream, const uint32_t *words, const float *scales, int layout,
+                       int block, int64_t K, int64_t N, float *w);
+
+/* y[M, N] = x[M, K] . W (+ bias[N]) with W the packed-Q4 weight in `layout`.
+ * Replaces QTensorOps::q_matmul's packed route (patches/burn-cubecl-0.21.0/src/ops/qtensor.rs:
+ * 303-368: f32 lhs, Q4S symmetric, f32 scales, PackedU32(0|1), block in {8,16,32,64,128}) and
+ * therefore linear_forward (crates/burn_boogu/src/model/linear.rs:14-37) and qwen_linear_forward
+ * (crates/burn_qwen3_vl/src/linear.rs:107-140).  x: row-major with row stride ldx elements
+ * (ldx >= K), dtype x_dtype in {F32, F16, BF16}; y: row-major, row stride N, y_dtype in
+ * {F32, F16, BF16}; bias may be NULL.  Requirements: K % 8 == 0, K % block == 0, N % 8 == 0,
+ * block in {8, 16, 32, 64, 128}.  Arithmetic: the signed nibbles are exact in f16, activations
+ * enter the matrix cores as f16 (f32 inputs as an exact-to-2^-22 f16 hi+lo pair), products
+ * accumulate in f32 per K-block, and each block sum is scaled by its f32 scale in f32. */
+int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                  const uint32_t *words, const float *scales, int layout, int block, int64_t N,
+                  const float *bias, void *y, int y_dtype);
+
+/* Exact attention O = softmax(Q K^T * scale + mask) V, the operator behind
+ * AttentionKernel::execute / execute_gqa (crates/burn_boogu/src/model/attention.rs:47-105), the
+ * padded-blackbox flash kernel (native_flash.rs:1006-1090) and Burn's attention op
+ * (patches/burn-cubecl-0.21.0/src/ops/module.rs:342-367), plus Qwen's causal text attention
+ * (crates/burn_qwen3_vl/src/text.rs:103-192) and per-frame vision attention (vision.rs:319-388).
+ *   q: [B, Hq, Sq, D] addressed by q_strides = {batch, head, seq} element strides (D contiguous),
+ *   k, v: [B, Hkv, Skv, D] with their strides, o: [B, Hq, Sq, D] with o_strides.  Token-major
+ *   [B, S, H, D] tensors are passed with strides {S*H*D, D, H*D}.
+ *   in_dtype in {F32, F16, BF16} for q, k and v; out_dtype in {F32, F16, BF16}.
+ *   Hq % Hkv == 0; query head h reads key/value head h / (Hq / Hkv).
+ *   D in {64, 128} or any multiple of 8 below 128 (computed in a zero-extended 128-wide tile,
+ *   e.g. the released D = 120 without a padded copy).
+ *   scale: softmax scale; scale <= 0 selects 1/sqrt(D).
+ *   causal != 0: key j is masked for query i when j > i (requires Sq == Skv).
+ *   cu_seqlens (device int32[nseg + 1], ascending, cu[0] = 0, cu[nseg] = Sq) or NULL: block-
+ *   diagonal segment mask over a packed sequence (requires Sq == Skv).
+ * Arithmetic: Q K^T on the matrix cores in bf16 (bf16 inputs) or f16 (f16 and f32 inputs, as the
+ * reference's F32->F16 bridge, attention.rs:406-497), f32 online softmax, P and V in f16 on the
+ * matrix cores, f32 accumulation. */
+int biq_attention(void *stream, const void *q, const void *k, const void *v, void *o,
+                  int in_dtype, int out_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
+                  int64_t Skv, int64_t D, const int64_t *q_strides, const int64_t *k_strides,
+                  const int64_t *v_strides, const int64_t *o_strides, float scale, int causal,
+                  const int32_t *cu_seqlens, int64_t nseg);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BIQ_H */

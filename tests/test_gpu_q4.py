@@ -1,0 +1,183 @@
+"""GPU parity of the Q4S format kernels and the packed-Q4 GEMM (through the C ABI) against the
+oracle.  Gate: dequantised weights and quantised bytes bit-exact; GEMM outputs max-abs <= 2e-3
+and mean|a-b|/mean|b| <= 1e-3 against the float64 oracle rounded to f32."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from gpu_util import assert_parity, dev, dev_words, host
+
+pytestmark = pytest.mark.gpu
+
+import burn_image_amd as B  # noqa: E402
+from burn_image_amd import workloads as W  # noqa: E402
+
+TORCH_DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def weight(words, scales, layout, block, K, N, device):
+    shape = (K, N) if layout == 1 else (N, K)
+    return B.from_packed(dev_words(words, device), dev(scales, device=device), layout, block, shape)
+
+
+@pytest.mark.parametrize("K,N", [(128, 128), (3360, 64), (24, 16), (13568, 24), (64, 3360)])
+def test_gpu_row_layout_quantizer_bit_exact(gpu, oracle, K, N):
+    rng = np.random.default_rng(K + N)
+    w = (rng.standard_normal((K, N)) * rng.uniform(0.01, 2.0, (1, N))).astype(np.float32)
+    w[:, 1] = 0.0
+    w[: min(K, 8), 2] = np.array([7.0, 3.5, -3.5, 2.5, -2.5, 0.5, -0.5, 0.0], np.float32)[: min(K, 8)]
+    q = B.quantize_row_layout_q4s_block_up_to128_f32(dev(w, device=gpu))
+    words, scales, blk = oracle.q4_quantize_kn(w)
+    assert q.block == blk
+    assert np.array_equal(host_words(q.words), words)
+    assert host(q.scales).tobytes() == scales.tobytes()
+
+
+def host_words(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("N,K", [(128, 128), (6144, 256), (3, 4096)])
+def test_gpu_qwen_quantizer_bit_exact(gpu, oracle, N, K):
+    rng = np.random.default_rng(N * 7 + K)
+    v = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    v[0, :128] = 0.0
+    q = B.quantize_q4s_block128_f32(dev(v, device=gpu))
+    words, scales = oracle.q4_quantize_nk(v)
+    assert np.array_equal(host_words(q.words), words)
+    assert host(q.scales).tobytes() == scales.tobytes()
+
+
+def test_gpu_quantizer_rejects_non_finite_and_bad_shapes(gpu):
+    w = torch.zeros((16, 8), device=gpu)
+    w[3, 2] = float("nan")
+    with pytest.raises(B.InvalidArgument, match="non-finite"):
+        B.quantize_row_layout_q4s_block_up_to128_f32(w)
+    with pytest.raises(B.InvalidArgument, match="no supported exact block"):
+        B.quantize_row_layout_q4s_block_up_to128_f32(torch.zeros((12, 8), device=gpu))
+    with pytest.raises(B.InvalidArgument, match="not divisible by 8"):
+        B.quantize_row_layout_q4s_block_up_to128_f32(torch.zeros((16, 12), device=gpu))
+    with pytest.raises(B.InvalidArgument, match="not divisible by 128"):
+        B.quantize_q4s_block128_f32(torch.zeros((2, 127), device=gpu))
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("block", [8, 16, 32, 64, 128])
+def test_gpu_dequant_bit_exact(gpu, oracle, layout, block):
+    K, N = 384, 200
+    words, scales = W.q4_weight(11, block * 2 + layout, K, N, layout=layout, block=block)
+    q = weight(words, scales, layout, block, K, N, gpu)
+    assert host(q.dequantize()).tobytes() == oracle.q4_dequant(words, scales, layout, block, K, N).tobytes()
+
+
+def test_gpu_kat_probe_reference(gpu):
+    """Browser probe KAT (runtime.rs:4737-4781): GPU-quantised exactly-representable weights,
+    f32 lhs; the reference gates max_abs <= 5e-4 against the f32 product."""
+    g = np.load(os.path.join(GOLDEN, "kat_probe.npz"), allow_pickle=False)
+    q = B.quantize_row_layout_q4s_block_up_to128_f32(dev(g["weight"], device=gpu))
+    assert np.array_equal(host_words(q.words), g["words"])
+    y = host(B.linear_forward(B.Linear(q), dev(g["lhs"], device=gpu)))
+    assert np.max(np.abs(y - g["expected"])) <= 5e-4
+    assert_parity(y, g["expected"].astype(np.float32), "kat_probe")
+
+
+@pytest.mark.parametrize("layout", [1, 0])
+def test_gpu_c1_linear_golden(gpu, layout):
+    g = np.load(os.path.join(GOLDEN, "c1_linear.npz"), allow_pickle=False)
+    tag = "kn" if layout == 1 else "nk"
+    q = weight(g[f"words_{tag}"], g[f"scales_{tag}"], layout, 128, 512, 512, gpu)
+    y = host(B.q_matmul(dev(g["x"], device=gpu), q))
+    assert_parity(y, g[f"y_{tag}"], f"c1_linear_{tag}")
+
+
+@pytest.mark.parametrize("layout", [1, 0])
+@pytest.mark.parametrize("block", [8, 16, 32, 64, 128])
+@pytest.mark.parametrize("xdt", ["bf16", "f32", "f16"])
+def test_gpu_q4_linear_blocks_dtypes_tails(gpu, oracle, layout, block, xdt):
+    M, K, N = 77, 640 if block != 8 else 648, 200
+    if layout == 0 and block != 128:
+        K = 640 if block != 8 else 648
+    x = W.activations(12, 1, M, K, xdt)
+    words, scales = W.q4_weight(12, 2 + block + layout, K, N, layout=layout, block=block)
+    q = weight(words, scales, layout, block, K, N, gpu)
+    y = host(B.q_matmul(dev(x, TORCH_DT[xdt], gpu), q))
+    ref = oracle.q4_linear_f64(x, words, scales, layout, block, N).astype(np.float32)
+    assert_parity(y, ref, f"blk{block}_l{layout}_{xdt}")
+
+
+def test_gpu_q4_linear_bias_and_output_dtypes(gpu, oracle):
+    M, K, N = 130, 256, 136
+    x = W.activations(13, 1, M, K, "bf16")
+    words, scales = W.q4_weight(13, 2, K, N, layout=1)
+    bias = np.linspace(-2, 2, N).astype(np.float32)
+    q = weight(words, scales, 1, 128, K, N, gpu)
+    ref = oracle.q4_linear_f64(x, words, scales, 1, 128, N, bias=bias).astype(np.float32)
+    lin = B.Linear(q, dev(bias, device=gpu))
+    xd = dev(x, torch.bfloat16, gpu)
+    assert_parity(host(B.linear_forward(lin, xd)), ref, "bias_f32")
+    y16 = host(B.linear_forward(lin, xd, out_dtype=torch.float16))
+    assert np.max(np.abs(y16 - ref)) <= np.max(np.abs(ref)) * 2.0 ** -10
+    yb = host(B.linear_forward(lin, xd, out_dtype=torch.bfloat16))
+    assert np.max(np.abs(yb - ref)) <= np.max(np.abs(ref)) * 2.0 ** -7
+    # rank-3 input keeps its leading shape
+    y3 = B.linear_forward(lin, xd[:128].reshape(2, 64, K))
+    assert tuple(y3.shape) == (2, 64, N)
+
+
+def sample_rows(M, n=40, seed=0):
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, n)]))
+
+
+@pytest.mark.parametrize("name", list(W.C3_SHAPES))
+def test_gpu_c3_projection_full_shape(gpu, oracle, name):
+    """C3 at M = 4608: sampled rows against the float64 oracle; every element against an fp32
+    product of the (bit-exact) dequantised weight; row-permutation equivariance bit-exact."""
+    K, N = W.C3_SHAPES[name]
+    M = 4608
+    idx = list(W.C3_SHAPES).index(name)
+    x = W.activations(3, 2 * idx, M, K, "bf16")
+    words, scales = W.q4_weight(3, 2 * idx + 1, K, N, layout=1)
+    q = weight(words, scales, 1, 128, K, N, gpu)
+    xd = dev(x, torch.bfloat16, gpu)
+    y = B.q_matmul(xd, q)
+    rows = sample_rows(M, seed=idx)
+    ref = oracle.q4_linear_f64(x, words, scales, 1, 128, N, rows=rows).astype(np.float32)
+    assert_parity(host(y[torch.from_numpy(rows).to(gpu)]), ref, f"c3_{name}_sampled")
+    with torch.no_grad():
+        full_ref = torch.matmul(xd.float(), q.dequantize())
+    assert_parity(host(y), host(full_ref), f"c3_{name}_full_vs_fp32")
+    perm = torch.randperm(M, generator=torch.Generator().manual_seed(idx)).to(gpu)
+    y_perm = B.q_matmul(xd[perm].contiguous(), q)
+    assert torch.equal(y_perm, y[perm])
+
+
+@pytest.mark.parametrize("name", list(W.C5_SHAPES))
+def test_gpu_c5_qwen_projection(gpu, oracle, name):
+    K, N = W.C5_SHAPES[name]
+    M = 1024
+    idx = list(W.C5_SHAPES).index(name)
+    x = W.activations(5, 4 + 2 * idx, M, K, "bf16")
+    words, scales = W.q4_weight(5, 5 + 2 * idx, K, N, layout=0)
+    q = weight(words, scales, 0, 128, K, N, gpu)
+    lin = B.Linear(q)
+    y = B.qwen_linear_forward(lin, dev(x, torch.bfloat16, gpu))
+    rows = sample_rows(M, seed=10 + idx)
+    ref = oracle.q4_linear_f64(x, words, scales, 0, 128, N, rows=rows).astype(np.float32)
+    assert_parity(host(y)[rows], ref, f"c5_{name}")
+
+
+def test_gpu_real_checkpoint_shapes(gpu, oracle):
+    """Released Boogu widths: K = 3360 (block 32) to N = 840 and 13568 -> 3360 (block 128)."""
+    for (K, N, seed) in ((3360, 840, 1), (13568, 3360, 2)):
+        blk = oracle.q4_kn_block(K, N)
+        M = 45
+        x = W.activations(14, seed, M, K, "f32")
+        words, scales = W.q4_weight(14, 10 + seed, K, N, layout=1, block=blk)
+        q = weight(words, scales, 1, blk, K, N, gpu)
+        y = host(B.q_matmul(dev(x, device=gpu), q))
+        ref = oracle.q4_linear_f64(x, words, scales, 1, blk, N).astype(np.float32)
+        assert_parity(y, ref, f"real_{K}x{N}_blk{blk}")
