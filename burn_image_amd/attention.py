@@ -128,3 +128,79 @@ class NativeQ4FlashAttention(AttentionKernel):
     with the dual-stream shared projection split (SplitDoubleStreamSharedProjection)."""
 
     SPLIT_DOUBLE_STREAM_SHARED_PROJECTION = True
+
+
+# ---------------------------------------------------------------------------------------------
+# Q/K RMSNorm + RoPE preparation (the seam's third method)
+# ---------------------------------------------------------------------------------------------
+
+STRICT_F32 = "strict_f32"
+F16_STORAGE_F32_ACCUM = "f16_storage_f32_accum"
+
+
+class RmsNorm:
+    """nn::RmsNorm parameters: gamma [D] and epsilon (crates/burn_boogu/src/model/norm.rs)."""
+
+    def __init__(self, gamma: torch.Tensor, epsilon: float = 1e-5):
+        self.gamma = gamma
+        self.epsilon = float(epsilon)
+
+
+def qk_norm_rope(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, norm_q: RmsNorm,
+                 norm_k: RmsNorm, cos: torch.Tensor, sin: torch.Tensor,
+                 out_dtype: torch.dtype = torch.float16, stream: Optional[int] = None):
+    """One fused HIP pass over token-major Q [B, S, Hq, D], K/V [B, S, Hkv, D]: strict-F32
+    RMSNorm + interleaved RoPE on Q and K, cast of all three to ``out_dtype``
+    (native_flash.rs:395-583).  cos/sin: [1 or B, S, D].  Returns contiguous (q, k, v)."""
+    B, S, Hq, D = query.shape
+    _, Sk, Hkv, _ = key.shape
+    if Sk != S or value.shape[1] != S:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG,
+                                   "fused strict Q/K norm+RoPE preparation requires equal Q/K sequence lengths")
+    if tuple(norm_q.gamma.shape) != (D,) or tuple(norm_k.gamma.shape) != (D,):
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "fused RMSNorm gamma width mismatch")
+    if cos.dim() != 3 or tuple(cos.shape[1:]) != (S, D) or cos.shape != sin.shape:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "fused RoPE tables must be [1|B, S, D]")
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if t.stride(3) != 1:
+            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, f"fused {name} head width must be contiguous")
+    if not (query.dtype == key.dtype == value.dtype) or query.dtype not in _DTYPE_CODE:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "fused Q/K/V dtype mismatch")
+    gq = norm_q.gamma.to(torch.float32).contiguous()
+    gk = norm_k.gamma.to(torch.float32).contiguous()
+    cs = cos.to(torch.float32).contiguous()
+    sn = sin.to(torch.float32).contiguous()
+    qo = torch.empty((B, S, Hq, D), dtype=out_dtype, device=query.device)
+    ko = torch.empty((B, S, Hkv, D), dtype=out_dtype, device=query.device)
+    vo = torch.empty((B, S, Hkv, D), dtype=out_dtype, device=query.device)
+    st = lambda t: _lib.strides3((t.stride(0), t.stride(1), t.stride(2)))
+    s = torch.cuda.current_stream(query.device).cuda_stream if stream is None else stream
+    _lib.check(_lib.load().biq_qk_norm_rope(
+        s, query.data_ptr(), key.data_ptr(), value.data_ptr(), _DTYPE_CODE[query.dtype],
+        B, S, Hq, Hkv, D, st(query), st(key), st(value), gq.data_ptr(), gk.data_ptr(),
+        norm_q.epsilon, norm_k.epsilon, cs.data_ptr(), sn.data_ptr(), cs.shape[0],
+        _DTYPE_CODE[out_dtype], qo.data_ptr(), ko.data_ptr(), vo.data_ptr()))
+    return qo, ko, vo
+
+
+def _execute_gqa_with_qk_norm_rope(cls, query, key, value, norm_q: RmsNorm, norm_k: RmsNorm,
+                                   rope, query_chunk_size: int,
+                                   rms_norm_policy: str = STRICT_F32,
+                                   operand_dtype: torch.dtype = torch.float16,
+                                   out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Normalise and rotate token-major Q/K, then grouped-query attention (attention.rs:107-134
+    seam; the packed-Q4 route of attention.rs:447-496).  Requires strict-F32 RMSNorm and RoPE
+    tables, as the reference's fused route asserts.  Output dtype defaults to the input dtype
+    (F32 projections in, F32 out)."""
+    if rms_norm_policy != STRICT_F32:
+        raise _lib.Unsupported(_lib.ERR_UNSUPPORTED,
+                               "packed-Q4 fused attention preparation requires strict-F32 RMSNorm")
+    if rope is None:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG,
+                                   "packed-Q4 fused attention preparation requires RoPE")
+    cos, sin = rope
+    q, k, v = qk_norm_rope(query, key, value, norm_q, norm_k, cos, sin, out_dtype=operand_dtype)
+    return cls.execute_gqa(q, k, v, query_chunk_size, out_dtype=out_dtype or query.dtype)
+
+
+AttentionKernel.execute_gqa_with_qk_norm_rope = classmethod(_execute_gqa_with_qk_norm_rope)
