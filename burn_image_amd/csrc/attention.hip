@@ -61,31 +61,6 @@ __device__ __forceinline__ u32x4_t load8_compute(const InT *p) {
   }
 }
 
-// 8 elements of V (InT) -> 8 f16 values (as floats for scattering).
-template <typename InT>
-__device__ __forceinline__ void load8_v_f16(const InT *p, _Float16 out[8]) {
-  if constexpr (sizeof(InT) == 4) {
-    const float4 *f = reinterpret_cast<const float4 *>(p);
-    float4 a = f[0], b = f[1];
-    out[0] = (_Float16)a.x; out[1] = (_Float16)a.y; out[2] = (_Float16)a.z; out[3] = (_Float16)a.w;
-    out[4] = (_Float16)b.x; out[5] = (_Float16)b.y; out[6] = (_Float16)b.z; out[7] = (_Float16)b.w;
-  } else if constexpr (std::is_same<InT, bf16_t>::value) {
-    u32x4_t v = *reinterpret_cast<const u32x4_t *>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[2 * i] = (_Float16)biq::bf16_lo_to_f32(v[i]);
-      out[2 * i + 1] = (_Float16)biq::bf16_hi_to_f32(v[i]);
-    }
-  } else {
-    u32x4_t v = *reinterpret_cast<const u32x4_t *>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[2 * i] = biq::bitcast<_Float16>((uint16_t)(v[i] & 0xffffu));
-      out[2 * i + 1] = biq::bitcast<_Float16>((uint16_t)(v[i] >> 16));
-    }
-  }
-}
-
 // Physical position of key c inside its 16-key group of the transposed V tile (swap bits 2, 3).
 __device__ __forceinline__ int vt_slot(int key) {
   return (key & ~15) | (key & 3) | ((key & 4) << 1) | ((key & 8) >> 1);
@@ -100,12 +75,32 @@ __device__ __forceinline__ int64_t segment_of(const int32_t *cu, int64_t nseg, i
   return lo;
 }
 
+// Per-thread register copy of one K/V tile (prefetched while the previous tile computes).
+template <int DP, typename InT>
+struct KVRegs {
+  static constexpr int K_CHUNKS = (BKV * DP / 8) / NTHREADS;  // 8-element K groups per thread
+  static constexpr int V_GROUPS = (BKV / 4) * (DP / 8);       // 4-key x 8-dim V blocks per tile
+  u32x4_t k16[K_CHUNKS];  // compute-type bits (f32 inputs are narrowed to f16 at load)
+  u32x4_t v16[4];         // input bits (bf16 / f16; f32 inputs narrowed to f16 at load)
+};
+
+// 8 f32 at p -> 8 f16 packed (f32 inputs take the reference's F32 -> F16 bridge at load).
+__device__ __forceinline__ u32x4_t load8_f32_as_f16(const float *p) {
+  const float4 *f = reinterpret_cast<const float4 *>(p);
+  const float4 a = f[0], b = f[1];
+  return u32x4_t{biq::pack_f16x2(a.x, a.y), biq::pack_f16x2(a.z, a.w), biq::pack_f16x2(b.x, b.y),
+                 biq::pack_f16x2(b.z, b.w)};
+}
+
 template <int DP, typename InT, int MASK>
 __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
   constexpr bool BF16 = std::is_same<InT, bf16_t>::value;
+  constexpr bool F32IN = sizeof(InT) == 4;
   constexpr int KS_LD = DP + 8;  // halves per row of the K tile
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[BKV * KS_LD];
-  __shared__ __attribute__((aligned(16))) _Float16 Vt[DP * VT_LD];
+  constexpr int K_CHUNKS = KVRegs<DP, InT>::K_CHUNKS;
+  constexpr int V_GROUPS = KVRegs<DP, InT>::V_GROUPS;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BKV * KS_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][DP * VT_LD];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -148,33 +143,94 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
     kv_end = kv_end < qlast + 1 ? kv_end : qlast + 1;
   }
   kv_begin = (kv_begin / BKV) * BKV;
+  const int64_t qmin = qblk + wave * 32, qmax = qmin + 31;  // this wave's query rows
+
+  // ---- global -> registers for the tile at kv0
+  auto load_tile = [&](int64_t kv0, KVRegs<DP, InT> &R) {
+#pragma unroll
+    for (int it = 0; it < K_CHUNKS; ++it) {
+      const int c = tid + it * NTHREADS;
+      const int row = c / (DP / 8), d0 = 8 * (c % (DP / 8));
+      const int64_t key = kv0 + row;
+      const bool ok = key < p.Skv && d0 < D;
+      if constexpr (F32IN)
+        R.k16[it] = ok ? load8_f32_as_f16(reinterpret_cast<const float *>(kg + key * p.ks[2] + d0))
+                       : u32x4_t{0u, 0u, 0u, 0u};
+      else
+        R.k16[it] = ok ? *reinterpret_cast<const u32x4_t *>(kg + key * p.ks[2] + d0)
+                       : u32x4_t{0u, 0u, 0u, 0u};
+    }
+    // V: thread owns keys 4 kb .. 4 kb + 3 at dims d0 .. d0 + 7 (key-consecutive lanes)
+    if (tid < V_GROUPS) {
+      const int kb = tid % (BKV / 4), d0 = 8 * (tid / (BKV / 4));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t key = kv0 + 4 * kb + j;
+        const bool ok = key < p.Skv && d0 < D;
+        if constexpr (F32IN)
+          R.v16[j] = ok ? load8_f32_as_f16(reinterpret_cast<const float *>(vg + key * p.vs[2] + d0))
+                        : u32x4_t{0u, 0u, 0u, 0u};
+        else
+          R.v16[j] = ok ? *reinterpret_cast<const u32x4_t *>(vg + key * p.vs[2] + d0)
+                        : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+
+  // ---- registers -> LDS buffer: K row-major in the compute type, V transposed f16
+  auto store_tile = [&](const KVRegs<DP, InT> &R, int buf) {
+#pragma unroll
+    for (int it = 0; it < K_CHUNKS; ++it) {
+      const int c = tid + it * NTHREADS;
+      const int row = c / (DP / 8), d0 = 8 * (c % (DP / 8));
+      *reinterpret_cast<u32x4_t *>(&Ks[buf][row * KS_LD + d0]) = R.k16[it];
+    }
+    if (tid < V_GROUPS) {
+      const int kb = tid % (BKV / 4), d0 = 8 * (tid / (BKV / 4));
+      // f16 values v[j][e] of key 4 kb + j, dim d0 + e
+      _Float16 vv[4][8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t w = R.v16[j][i];
+          if constexpr (BF16) {
+            vv[j][2 * i] = (_Float16)biq::bf16_lo_to_f32(w);
+            vv[j][2 * i + 1] = (_Float16)biq::bf16_hi_to_f32(w);
+          } else {
+            vv[j][2 * i] = biq::bitcast<_Float16>((uint16_t)(w & 0xffffu));
+            vv[j][2 * i + 1] = biq::bitcast<_Float16>((uint16_t)(w >> 16));
+          }
+        }
+      }
+      const int slot = vt_slot(4 * kb);  // the 4 keys keep consecutive slots
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        half2_t lo = {vv[0][e], vv[1][e]}, hi = {vv[2][e], vv[3][e]};
+        uint2 w = make_uint2(biq::bitcast<uint32_t>(lo), biq::bitcast<uint32_t>(hi));
+        *reinterpret_cast<uint2 *>(&Vt[buf][(d0 + e) * VT_LD + slot]) = w;
+      }
+    }
+  };
 
   floatx16_t oacc[DP / 32];
 #pragma unroll
   for (int i = 0; i < DP / 32; ++i) oacc[i] = biq::zero16();
+  // m_run: reference maximum (log2 domain) the running sums are relative to; it only moves
+  // when a new score exceeds it by more than 2^8, so most tiles skip the O rescale.
   float m_run = -INFINITY, l_run = 0.0f;
 
-  for (int64_t kv0 = kv_begin; kv0 < kv_end; kv0 += BKV) {
-    __syncthreads();
-    // ---- stage K (compute type, row-major) and V (f16, transposed + slot-permuted)
-#pragma unroll
-    for (int it = 0; it < (BKV * DP / 8) / NTHREADS; ++it) {
-      const int c = tid + it * NTHREADS;
-      const int row = c / (DP / 8), ch = c % (DP / 8);
-      const int64_t key = kv0 + row;
-      const int d0 = 8 * ch;
-      u32x4_t kv = {0u, 0u, 0u, 0u};
-      _Float16 vv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (key < p.Skv && d0 < D) {
-        kv = load8_compute<InT, BF16>(kg + key * p.ks[2] + d0);
-        load8_v_f16<InT>(vg + key * p.vs[2] + d0, vv);
-      }
-      *reinterpret_cast<u32x4_t *>(&Ks[row * KS_LD + d0]) = kv;
-      const int slot = vt_slot(row);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[(d0 + e) * VT_LD + slot] = vv[e];
-    }
-    __syncthreads();
+  KVRegs<DP, InT> R;
+  int buf = 0;
+  if (kv_begin < kv_end) {
+    load_tile(kv_begin, R);
+    store_tile(R, 0);
+  }
+  __syncthreads();
+
+  for (int64_t kv0 = kv_begin; kv0 < kv_end; kv0 += BKV, buf ^= 1) {
+    const bool has_next = kv0 + BKV < kv_end;
+    if (has_next) load_tile(kv0 + BKV, R);
 
     // ---- S^T = K Q^T for the tile's 64 keys (2 x 32)
     floatx16_t sacc[2];
@@ -183,8 +239,8 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
       floatx16_t a = biq::zero16();
 #pragma unroll
       for (int s = 0; s < DP / 16; ++s) {
-        const u32x4_t kf =
-            *reinterpret_cast<const u32x4_t *>(&Ks[(32 * ks + l32) * KS_LD + 16 * s + 8 * lh]);
+        const u32x4_t kf = *reinterpret_cast<const u32x4_t *>(
+            &Ks[buf][(32 * ks + l32) * KS_LD + 16 * s + 8 * lh]);
         if constexpr (BF16)
           a = biq::mfma32x32x16_bf16(biq::bitcast<bf16x8_t>(kf), biq::bitcast<bf16x8_t>(qf[s]), a);
         else
@@ -193,25 +249,48 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
       sacc[ks] = a;
     }
 
-    // ---- scale, mask, online softmax (base 2)
+    // ---- scale (log2 domain), mask where the tile needs it, row max
+    bool need_mask = kv0 + BKV > p.Skv;
+    if constexpr (MASK & MASK_SEGMENT) need_mask = true;
+    if constexpr (MASK & MASK_CAUSAL) need_mask = need_mask || (kv0 + BKV - 1 > qmin);
     float mx = -INFINITY;
+    if (need_mask) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t key = kv0 + 32 * ks + 8 * (r >> 2) + 4 * lh + (r & 3);
-        bool ok = key < p.Skv;
-        if constexpr (MASK & MASK_SEGMENT) ok = ok && key >= seg_lo && key < seg_hi;
-        if constexpr (MASK & MASK_CAUSAL) ok = ok && key <= qi;
-        const float x = ok ? sacc[ks][r] * p.scale_log2 : -INFINITY;
-        sacc[ks][r] = x;
-        mx = fmaxf(mx, x);
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int64_t key = kv0 + 32 * ks + 8 * (r >> 2) + 4 * lh + (r & 3);
+          bool ok = key < p.Skv;
+          if constexpr (MASK & MASK_SEGMENT) ok = ok && key >= seg_lo && key < seg_hi;
+          if constexpr (MASK & MASK_CAUSAL) ok = ok && key <= qi;
+          const float x = ok ? sacc[ks][r] * p.scale_log2 : -INFINITY;
+          sacc[ks][r] = x;
+          mx = fmaxf(mx, x);
+        }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float x = sacc[ks][r] * p.scale_log2;
+          sacc[ks][r] = x;
+          mx = fmaxf(mx, x);
+        }
+    }
+    (void)qmax;
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
+    // ---- move the reference maximum only when it grows by more than 2^8 (exact: O and l
+    //      are both relative to the same reference)
+    const bool grow = mx > m_run + 8.0f;
+    if (__any(grow)) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < DP / 32; ++i) oacc[i] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
     float rs = 0.0f;
     u32x4_t pf[4];  // P^T as f16 B operands of the four 16-key steps
 #pragma unroll
@@ -225,9 +304,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
           rs += e0 + e1;
           pf[2 * ks + t][j] = biq::pack_f16x2(e0, e1);
         }
-    l_run = l_run * alpha + rs;
-#pragma unroll
-    for (int i = 0; i < DP / 32; ++i) oacc[i] *= alpha;
+    l_run += rs;
 
     // ---- O^T += V^T P^T
 #pragma unroll
@@ -235,11 +312,14 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
       const half8_t bp = biq::bitcast<half8_t>(pf[t]);
 #pragma unroll
       for (int i = 0; i < DP / 32; ++i) {
-        const half8_t av =
-            *reinterpret_cast<const half8_t *>(&Vt[(32 * i + l32) * VT_LD + 16 * t + 8 * lh]);
+        const half8_t av = *reinterpret_cast<const half8_t *>(
+            &Vt[buf][(32 * i + l32) * VT_LD + 16 * t + 8 * lh]);
         oacc[i] = biq::mfma32x32x16_f16(av, bp, oacc[i]);
       }
     }
+
+    if (has_next) store_tile(R, buf ^ 1);
+    __syncthreads();
   }
 
   // ---- normalise and store O[b, h, qi, d]

@@ -17,15 +17,22 @@
 //    accumulator and added to the output accumulator as acc += scale[b, n] * partial in f32,
 //    so the f32 block scale is never rounded to 16 bits.
 //
-// Tiling: 256 threads = 4 waves in a 2 x 2 grid, workgroup tile 128 x 128, wave tile 64 x 64
-// (2 x 2 MFMA 32 x 32 tiles), K staged 64 at a time through LDS.
+// Schedule: 512 threads = 8 waves (2 per SIMD) in a 2 (M) x 4 (N) grid; workgroup tile
+// 128 x 256, wave tile 64 x 64 (2 x 2 MFMA 32 x 32 tiles); K advances 64 per tile.  While the
+// waves run the MFMAs of tile t from one LDS buffer, every thread already holds tile t+1's global
+// loads (activations, packed words and block scales) in registers; it converts and stores them
+// into the other LDS buffer afterwards, so one barrier per tile separates the two.  Workgroups are
+// numbered so that each XCD (hardware places workgroup i on XCD i % 8) walks a compact,
+// M-grouped block of output tiles, keeping the shared activation and weight tiles in its L2.
 #include "common.h"
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64, NTHREADS = 256;
+constexpr int BM = 128, BN = 256, BK = 64, NTHREADS = 512;
+constexpr int WAVES_N = 4;
 constexpr int A_LD = BK + 8;  // LDS row stride of the activation tile, in halves (16 B pad)
 constexpr int B_LD = BN;      // LDS row stride of the word tile, in words
+constexpr int GROUP_M = 8;    // M tiles per raster group
 
 enum XMode { XM_F16 = 0, XM_BF16 = 1, XM_F32 = 2 };
 
@@ -89,22 +96,123 @@ __device__ __forceinline__ float load_scale(const float *__restrict__ scales, in
   return LAYOUT == BIQ_Q4_KN_AXIS1 ? scales[b * N + n] : scales[n * nblk + b];
 }
 
+// Per-thread register copy of one tile's global data.
+template <int XMODE>
+struct TileRegs {
+  static constexpr int A_CHUNKS = (BM * BK / 8) / NTHREADS;  // 8-element groups per thread
+  u32x4_t a16[XMODE == XM_F32 ? 1 : A_CHUNKS];
+  float4 a32[XMODE == XM_F32 ? 2 * A_CHUNKS : 1];
+  u32x4_t b;
+};
+
 template <int LAYOUT, int XMODE, int BLK>
 __global__ void __launch_bounds__(NTHREADS, 1)
     q4_gemm_kernel(const void *__restrict__ xv, int64_t ldx, const uint32_t *__restrict__ words,
                    const float *__restrict__ scales, const float *__restrict__ bias,
-                   void *__restrict__ yv, int y_dtype, int64_t M, int64_t N, int64_t K) {
+                   void *__restrict__ yv, int y_dtype, int64_t M, int64_t N, int64_t K,
+                   int tiles_m, int tiles_n) {
   constexpr int NSPLIT = XMODE == XM_F32 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) uint16_t As[NSPLIT][BM * A_LD];
-  __shared__ __attribute__((aligned(16))) uint32_t Bs[(BK / 8) * B_LD];
+  constexpr int A_CHUNKS = TileRegs<XMODE>::A_CHUNKS;
+  constexpr int TILE_BLOCKS = BLK >= BK ? 1 : BK / BLK;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][NSPLIT][BM * A_LD];
+  __shared__ __attribute__((aligned(16))) uint32_t Bs[2][(BK / 8) * B_LD];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int l32 = lane & 31, lh = lane >> 5;
-  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+
+  // ---- XCD-aware, M-grouped tile order
+  int64_t pid;
+  {
+    const int64_t T = (int64_t)tiles_m * tiles_n;
+    const int64_t L = blockIdx.x;
+    const int64_t q = T / 8, r = T % 8, xcd = L % 8, slot = L / 8;
+    pid = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+  }
+  const int64_t in_group = (int64_t)GROUP_M * tiles_n;
+  const int64_t first_m = (pid / in_group) * GROUP_M;
+  const int64_t gsize = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
+  const int64_t tile_m = first_m + (pid % in_group) % gsize;
+  const int64_t tile_n = (pid % in_group) / gsize;
+  const int64_t m0 = tile_m * BM, n0 = tile_n * BN;
   const int64_t nblk = K / BLK;
   const int64_t KW = K / 8;
+
+  int64_t ncol[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) ncol[j] = n0 + wn * 64 + 32 * j + l32;
+
+  // ---- global -> registers for one K tile
+  auto load_tile = [&](int64_t kt, TileRegs<XMODE> &R, float (&sc)[2][TILE_BLOCKS]) {
+#pragma unroll
+    for (int it = 0; it < A_CHUNKS; ++it) {
+      const int c = tid + it * NTHREADS;
+      const int row = c >> 3, kc = c & 7;
+      const int64_t gm = m0 + row, gk = kt + 8 * kc;
+      const bool ok = gm < M && gk < K;
+      if constexpr (XMODE == XM_F32) {
+        const float4 *src =
+            reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(xv) + gm * ldx + gk);
+        R.a32[2 * it] = ok ? src[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+        R.a32[2 * it + 1] = ok ? src[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        R.a16[it] = ok ? *reinterpret_cast<const u32x4_t *>(
+                             reinterpret_cast<const uint16_t *>(xv) + gm * ldx + gk)
+                       : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+    const int64_t kw0 = kt / 8;
+    if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
+      const int kwr = tid >> 6, nc = (tid & 63) * 4;
+      R.b = (kw0 + kwr < KW && n0 + nc < N)
+                ? *reinterpret_cast<const u32x4_t *>(words + (kw0 + kwr) * N + n0 + nc)
+                : u32x4_t{0u, 0u, 0u, 0u};
+    } else {
+      const int nl = tid >> 1, half = tid & 1;
+      const int64_t n = n0 + nl, kwb = kw0 + 4 * half;
+      u32x4_t w = {0u, 0u, 0u, 0u};
+      if (n < N) {
+        const uint32_t *src = words + n * KW + kwb;
+        if ((KW & 3) == 0 && kwb + 3 < KW) {
+          w = *reinterpret_cast<const u32x4_t *>(src);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (kwb + j < KW) w[j] = src[j];
+        }
+      }
+      R.b = w;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int t = 0; t < TILE_BLOCKS; ++t)
+        sc[j][t] = load_scale<LAYOUT>(scales, kt / BLK + t, ncol[j], N, nblk);
+  };
+
+  // ---- registers -> LDS buffer (activation conversion to f16 slot order happens here)
+  auto store_tile = [&](const TileRegs<XMODE> &R, int buf) {
+#pragma unroll
+    for (int it = 0; it < A_CHUNKS; ++it) {
+      const int c = tid + it * NTHREADS;
+      const int row = c >> 3, kc = c & 7;
+      u32x4_t hi, lo;
+      if constexpr (XMODE == XM_BF16) hi = bf16x8_to_f16_slots(R.a16[it]);
+      else if constexpr (XMODE == XM_F16) hi = f16x8_to_slots(R.a16[it]);
+      else f32x8_to_f16_split_slots(R.a32[2 * it], R.a32[2 * it + 1], hi, lo);
+      *reinterpret_cast<u32x4_t *>(&As[buf][0][row * A_LD + 8 * kc]) = hi;
+      if constexpr (NSPLIT == 2) *reinterpret_cast<u32x4_t *>(&As[buf][1][row * A_LD + 8 * kc]) = lo;
+    }
+    if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
+      const int kwr = tid >> 6, nc = (tid & 63) * 4;
+      *reinterpret_cast<u32x4_t *>(&Bs[buf][kwr * B_LD + nc]) = R.b;
+    } else {
+      const int nl = tid >> 1, half = tid & 1;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Bs[buf][(4 * half + j) * B_LD + nl] = R.b[j];
+    }
+  };
 
   floatx16_t acc[2][2], part[2][2];
 #pragma unroll
@@ -115,78 +223,18 @@ __global__ void __launch_bounds__(NTHREADS, 1)
       part[i][j] = biq::zero16();
     }
 
-  int64_t ncol[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) ncol[j] = n0 + wn * 64 + 32 * j + l32;
+  TileRegs<XMODE> R;
+  float sc[2][TILE_BLOCKS], sc_next[2][TILE_BLOCKS];
+  load_tile(0, R, sc);
+  store_tile(R, 0);
+  __syncthreads();
 
-  for (int64_t kt = 0; kt < K; kt += BK) {
-    // ---------------- stage the activation tile (BM x BK) into LDS as f16 slots -------------
-#pragma unroll
-    for (int it = 0; it < (BM * BK / 8) / NTHREADS; ++it) {
-      const int c = tid + it * NTHREADS;
-      const int row = c >> 3, kc = c & 7;
-      const int64_t gm = m0 + row, gk = kt + 8 * kc;
-      u32x4_t hi = {0u, 0u, 0u, 0u}, lo = {0u, 0u, 0u, 0u};
-      if (gm < M && gk < K) {
-        if constexpr (XMODE == XM_BF16) {
-          const u32x4_t v = *reinterpret_cast<const u32x4_t *>(
-              reinterpret_cast<const uint16_t *>(xv) + gm * ldx + gk);
-          hi = bf16x8_to_f16_slots(v);
-        } else if constexpr (XMODE == XM_F16) {
-          const u32x4_t v = *reinterpret_cast<const u32x4_t *>(
-              reinterpret_cast<const uint16_t *>(xv) + gm * ldx + gk);
-          hi = f16x8_to_slots(v);
-        } else {
-          const float4 *src =
-              reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(xv) + gm * ldx + gk);
-          f32x8_to_f16_split_slots(src[0], src[1], hi, lo);
-        }
-      }
-      *reinterpret_cast<u32x4_t *>(&As[0][row * A_LD + 8 * kc]) = hi;
-      if constexpr (NSPLIT == 2) *reinterpret_cast<u32x4_t *>(&As[1][row * A_LD + 8 * kc]) = lo;
-    }
-    // ---------------- stage the packed word tile (BK/8 x BN words) into LDS -----------------
-    {
-      const int64_t kw0 = kt / 8;
-      if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
-        const int kwr = tid >> 5, nc = (tid & 31) * 4;
-        u32x4_t w = {0u, 0u, 0u, 0u};
-        if (kw0 + kwr < KW && n0 + nc < N)
-          w = *reinterpret_cast<const u32x4_t *>(words + (kw0 + kwr) * N + n0 + nc);
-        *reinterpret_cast<u32x4_t *>(&Bs[kwr * B_LD + nc]) = w;
-      } else {
-        const int nl = tid >> 1, half = tid & 1;
-        const int64_t n = n0 + nl;
-        uint32_t w[4] = {0u, 0u, 0u, 0u};
-        if (n < N) {
-          const int64_t kwb = kw0 + 4 * half;
-          const uint32_t *src = words + n * KW + kwb;
-          if ((KW & 3) == 0 && kwb + 3 < KW) {
-            const u32x4_t v = *reinterpret_cast<const u32x4_t *>(src);
-            w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
-          } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (kwb + j < KW) w[j] = src[j];
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) Bs[(4 * half + j) * B_LD + nl] = w[j];
-      }
-    }
-    // per-tile scales: every block that ends inside this tile
-    constexpr int TILE_BLOCKS = BLK >= BK ? 1 : BK / BLK;
-    constexpr int SCALES_PER_TILE = BLK == 8 ? TILE_BLOCKS : TILE_BLOCKS;
-    float sc[2][SCALES_PER_TILE];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int t = 0; t < SCALES_PER_TILE; ++t)
-        sc[j][t] = load_scale<LAYOUT>(scales, kt / BLK + t, ncol[j], N, nblk);
+  int buf = 0;
+  for (int64_t kt = 0; kt < K; kt += BK, buf ^= 1) {
+    const bool has_next = kt + BK < K;
+    if (has_next) load_tile(kt + BK, R, sc_next);
 
-    __syncthreads();
-
-    // ---------------- MFMA over the 4 K16 steps of the tile --------------------------------
+    // ---------------- MFMA over the 4 K16 steps of tile kt ---------------------------------
 #pragma unroll
     for (int s = 0; s < BK / 16; ++s) {
       if (kt + 16 * s >= K) break;
@@ -196,14 +244,14 @@ __global__ void __launch_bounds__(NTHREADS, 1)
 #pragma unroll
         for (int x = 0; x < NSPLIT; ++x)
           a[i][x] = *reinterpret_cast<const half8_t *>(
-              &As[x][(wm * 64 + 32 * i + l32) * A_LD + 16 * s + 8 * lh]);
+              &As[buf][x][(wm * 64 + 32 * i + l32) * A_LD + 16 * s + 8 * lh]);
       half8_t bq[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        bq[j] = unpack_q4_f16(Bs[(2 * s + lh) * B_LD + wn * 64 + 32 * j + l32]);
+        bq[j] = unpack_q4_f16(Bs[buf][(2 * s + lh) * B_LD + wn * 64 + 32 * j + l32]);
 
       if constexpr (BLK == 8) {
-        // Lanes 0-31 carry block 2g, lanes 32-63 block 2g + 1: two masked MFMAs per tile.
+        // Lanes 0-31 carry block 2g, lanes 32-63 block 2g + 1: two masked MFMAs.
         const half8_t zh = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -222,7 +270,7 @@ __global__ void __launch_bounds__(NTHREADS, 1)
       } else {
         constexpr int SPB = BLK / 16;  // K16 steps per block
         bool first, last;
-        int tb;  // index of this step's block within the tile's scale list
+        int tb;
         if constexpr (BLK >= BK) {
           first = (s == 0) && (kt % BLK == 0);
           last = (s == BK / 16 - 1) && ((kt + BK) % BLK == 0);
@@ -232,15 +280,25 @@ __global__ void __launch_bounds__(NTHREADS, 1)
           last = (s % SPB) == SPB - 1;
           tb = s / SPB;
         }
+        if (first) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+          for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            floatx16_t p = first ? biq::zero16() : part[i][j];
-            p = biq::mfma32x32x16_f16(a[i][0], bq[j], p);
-            if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a[i][1], bq[j], p);
-            part[i][j] = p;
-          }
+            for (int j = 0; j < 2; ++j) {
+              floatx16_t p = biq::mfma32x32x16_f16(a[i][0], bq[j], biq::zero16());
+              if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a[i][1], bq[j], p);
+              part[i][j] = p;
+            }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              floatx16_t p = biq::mfma32x32x16_f16(a[i][0], bq[j], part[i][j]);
+              if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a[i][1], bq[j], p);
+              part[i][j] = p;
+            }
+        }
         if (last) {
 #pragma unroll
           for (int i = 0; i < 2; ++i)
@@ -248,6 +306,14 @@ __global__ void __launch_bounds__(NTHREADS, 1)
             for (int j = 0; j < 2; ++j) acc[i][j] += sc[j][tb] * part[i][j];
         }
       }
+    }
+
+    if (has_next) {
+      store_tile(R, buf ^ 1);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int t = 0; t < TILE_BLOCKS; ++t) sc[j][t] = sc_next[j][t];
     }
     __syncthreads();
   }
@@ -280,30 +346,20 @@ template <int LAYOUT, int XMODE>
 int launch_blk(hipStream_t s, int block, const void *x, int64_t ldx, const uint32_t *words,
                const float *scales, const float *bias, void *y, int y_dtype, int64_t M, int64_t N,
                int64_t K) {
-  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+  const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
+  dim3 grid((unsigned)((int64_t)tiles_m * tiles_n));
   dim3 blk(NTHREADS);
+#define BIQ_LAUNCH(B)                                                                              \
+  hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, B>), grid, blk, 0, s, x, ldx, words, scales,  \
+                     bias, y, y_dtype, M, N, K, tiles_m, tiles_n)
   switch (block) {
-    case 8:
-      hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, 8>), grid, blk, 0, s, x, ldx, words,
-                         scales, bias, y, y_dtype, M, N, K);
-      break;
-    case 16:
-      hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, 16>), grid, blk, 0, s, x, ldx, words,
-                         scales, bias, y, y_dtype, M, N, K);
-      break;
-    case 32:
-      hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, 32>), grid, blk, 0, s, x, ldx, words,
-                         scales, bias, y, y_dtype, M, N, K);
-      break;
-    case 64:
-      hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, 64>), grid, blk, 0, s, x, ldx, words,
-                         scales, bias, y, y_dtype, M, N, K);
-      break;
-    default:
-      hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, 128>), grid, blk, 0, s, x, ldx, words,
-                         scales, bias, y, y_dtype, M, N, K);
-      break;
+    case 8: BIQ_LAUNCH(8); break;
+    case 16: BIQ_LAUNCH(16); break;
+    case 32: BIQ_LAUNCH(32); break;
+    case 64: BIQ_LAUNCH(64); break;
+    default: BIQ_LAUNCH(128); break;
   }
+#undef BIQ_LAUNCH
   return biq::check_launch("q4 linear");
 }
 
@@ -346,8 +402,9 @@ extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M
       (reinterpret_cast<uintptr_t>(words) & 15) || (reinterpret_cast<uintptr_t>(scales) & 3))
     return biq::fail(BIQ_ERR_INVALID_ARG,
                      "q4 linear requires 16-byte aligned activation rows and packed words");
-  if (M > (int64_t)65535 * 128)
-    return biq::fail(BIQ_ERR_UNSUPPORTED, "q4 linear supports at most 8388480 rows per call");
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  if (tiles > 0x7fffffffLL)
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "q4 linear output has too many tiles for one launch");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (layout == BIQ_Q4_KN_AXIS1)
     return launch_layout<BIQ_Q4_KN_AXIS1>(s, x_dtype, block, x, ldx, words, scales, bias, y, y_dtype,

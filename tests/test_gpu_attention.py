@@ -139,3 +139,60 @@ def test_gpu_invalid_arguments_fail_closed(gpu):
         B.attention(x, k3, k3)
     with pytest.raises(B.InvalidArgument):
         B.AttentionKernel.execute(x, x, x, 0)
+
+
+def _prep_inputs(S=160, Hq=4, Hkv=2, D=120, seed=31):
+    from burn_image_amd import rope as R
+    rng = np.random.default_rng(seed)
+    q = (rng.standard_normal((1, S, Hq, D)) * 2.0).astype(np.float32)
+    k = (rng.standard_normal((1, S, Hkv, D)) * 0.5).astype(np.float32)
+    v = rng.standard_normal((1, S, Hkv, D)).astype(np.float32)
+    gq = (1.0 + 0.25 * rng.standard_normal(D)).astype(np.float32)
+    gk = (1.0 + 0.25 * rng.standard_normal(D)).astype(np.float32)
+    ids = R.position_ids(32, [], (40, 40), 2)[:S]
+    cos, sin = R.rope_values(ids, [40, 40, 40] if D == 120 else [32, 48, 48], 1.0e4)
+    return q, k, v, gq, gk, cos, sin
+
+
+def test_gpu_qk_norm_rope_prep_matches_oracle(gpu, oracle):
+    """Fused strict-F32 RMSNorm + interleaved RoPE + f16 cast (native_flash.rs:395-583) against
+    the oracle's composition rms_norm -> apply_rope -> f16; differences stay within one f16
+    rounding of the value."""
+    q, k, v, gq, gk, cos, sin = _prep_inputs()
+    norm_q = B.RmsNorm(dev(gq, device=gpu), 1e-5)
+    norm_k = B.RmsNorm(dev(gk, device=gpu), 1e-5)
+    qo, ko, vo = B.qk_norm_rope(dev(q, device=gpu), dev(k, device=gpu), dev(v, device=gpu),
+                                          norm_q, norm_k, dev(cos[None], device=gpu),
+                                          dev(sin[None], device=gpu))
+    assert qo.dtype == torch.float16 and tuple(qo.shape) == q.shape
+    for name, x, g, out in (("q", q, gq, qo), ("k", k, gk, ko)):
+        exp = oracle.apply_rope_interleaved(oracle.rms_norm(x, g, 1e-5), np.broadcast_to(cos[None, :, None, :], x.shape),
+                                            np.broadcast_to(sin[None, :, None, :], x.shape))
+        got = host(out)
+        tol = np.abs(exp) * 2.0 ** -10 + 1e-6
+        assert np.all(np.abs(got - exp) <= tol), f"{name}: {np.max(np.abs(got - exp) - tol)}"
+    assert np.array_equal(host(vo), W.round_to_f16(v))
+
+
+def test_gpu_execute_gqa_with_qk_norm_rope_matches_composition(gpu, oracle):
+    """The seam's third method (attention.rs:107-134; packed-Q4 route :447-496): F32 raw
+    projections in, F32 attention out, against the float64 oracle of norm -> RoPE -> GQA attention."""
+    q, k, v, gq, gk, cos, sin = _prep_inputs(S=300, Hq=28, Hkv=7, D=120, seed=32)
+    out = B.NativeQ4FlashAttention.execute_gqa_with_qk_norm_rope(
+        dev(q, device=gpu), dev(k, device=gpu), dev(v, device=gpu),
+        B.RmsNorm(dev(gq, device=gpu), 1e-5), B.RmsNorm(dev(gk, device=gpu), 1e-5),
+        (dev(cos[None], device=gpu), dev(sin[None], device=gpu)), 8192)
+    assert out.dtype == torch.float32 and tuple(out.shape) == q.shape
+    cs = np.broadcast_to(cos[None, :, None, :], q.shape)
+    sn = np.broadcast_to(sin[None, :, None, :], q.shape)
+    qn = oracle.apply_rope_interleaved(oracle.rms_norm(q, gq, 1e-5), cs, sn)
+    kn = oracle.apply_rope_interleaved(oracle.rms_norm(k, gk, 1e-5), cs[:, :, :7], sn[:, :, :7])
+    ref = oracle.attention_f64(qn.transpose(0, 2, 1, 3), kn.transpose(0, 2, 1, 3),
+                               v.transpose(0, 2, 1, 3)).transpose(0, 2, 1, 3).astype(np.float32)
+    assert_parity(host(out), ref, "execute_gqa_with_qk_norm_rope")
+    with pytest.raises(B.Unsupported):
+        B.NativeQ4FlashAttention.execute_gqa_with_qk_norm_rope(
+            dev(q, device=gpu), dev(k, device=gpu), dev(v, device=gpu),
+            B.RmsNorm(dev(gq, device=gpu)), B.RmsNorm(dev(gk, device=gpu)),
+            (dev(cos[None], device=gpu), dev(sin[None], device=gpu)), 8192,
+            rms_norm_policy=B.F16_STORAGE_F32_ACCUM)
