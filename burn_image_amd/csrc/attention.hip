@@ -283,9 +283,10 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
     //      are both relative to the same reference)
     const bool grow = mx > m_run + 8.0f;
     if (__any(grow)) {
-      const float m_new = grow ? mx : m_run;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
-      m_run = m_new;
+      // Lanes that do not grow keep alpha = 1 exactly (their m_run may still be -inf when all
+      // keys seen so far were masked, and -inf - -inf must not reach exp2).
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;  // 0 if m_run = -inf
+      m_run = grow ? mx : m_run;
       l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < DP / 32; ++i) oacc[i] *= alpha;

@@ -1,0 +1,158 @@
+"""Per-operator microbenchmarks of libbiq on one GPU (HIP-event timing, JSON output).
+
+    python -m burn_image_amd.perf q4_linear --M 4608 --K 3072 --N 9216 [--layout 1] [--block 128]
+                                            [--xdtype bf16] [--ydtype f32] [--iters 50]
+    python -m burn_image_amd.perf attention --B 1 --H 24 --Hkv 24 --S 4608 --D 128 [--dtype bf16]
+                                            [--causal] [--segments 1024:64:512]
+    python -m burn_image_amd.perf qk_prep --S 4608 --Hq 24 --Hkv 24 --D 128 [--dtype f32]
+
+Inputs are random and resident on the GPU before timing; weights rotate over enough distinct
+copies (``--rotate-bytes``, default 0) to defeat the 256 MB MALL when measuring HBM-bound shapes.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+import numpy as np
+import torch
+
+from . import _lib
+from .attention import RmsNorm, attention, qk_norm_rope
+from .linear import q_matmul
+from .q4 import from_packed
+
+DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+PEAK_TFLOPS = 2500.0
+PEAK_GBS = 8000.0
+
+
+def _time(fn, iters: int, warmup: int) -> float:
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(iters):
+        fn(i)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters * 1e3  # microseconds
+
+
+def bench_q4_linear(a) -> dict:
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    K, N, M = a.K, a.N, a.M
+    wshape = (K // 8, N) if a.layout == 1 else (N, K // 8)
+    sshape = (K // a.block, N) if a.layout == 1 else (N, K // a.block)
+    wbytes = K * N // 2 + (K // a.block) * N * 4
+    copies = max(1, int(np.ceil(a.rotate_bytes / wbytes))) if a.rotate_bytes else 1
+    weights = []
+    for _ in range(copies):
+        words = torch.randint(-2 ** 31, 2 ** 31 - 1, wshape, dtype=torch.int32, device=dev, generator=g)
+        scales = torch.rand(sshape, device=dev, generator=g) * 0.015 + 0.005
+        weights.append(from_packed(words, scales, a.layout, a.block, (K, N) if a.layout == 1 else (N, K)))
+    x = torch.randn((M, K), device=dev, generator=g).to(DT[a.xdtype])
+    y = torch.empty((M, N), dtype=DT[a.ydtype], device=dev)
+    us = _time(lambda i: q_matmul(x, weights[i % copies], out=y), a.iters, a.warmup)
+    flops = 2.0 * M * N * K
+    ebytes = {"f32": 4, "f16": 2, "bf16": 2}
+    bytes_ = wbytes + M * K * ebytes[a.xdtype] + M * N * ebytes[a.ydtype]
+    return {"op": "q4_linear", "M": M, "K": K, "N": N, "layout": a.layout, "block": a.block,
+            "xdtype": a.xdtype, "ydtype": a.ydtype, "weight_copies": copies, "us": round(us, 3),
+            "tflops": round(flops / us / 1e6, 2), "frac_mfma_peak": round(flops / us / 1e6 / PEAK_TFLOPS, 4),
+            "gbs": round(bytes_ / us / 1e3, 1), "frac_hbm_peak": round(bytes_ / us / 1e3 / PEAK_GBS, 4)}
+
+
+def _segments(spec: str, S: int) -> np.ndarray:
+    total, lo, hi = (int(v) for v in spec.split(":"))
+    from .workloads import c5_segments
+    return c5_segments(total if total else S, lo, hi)
+
+
+def bench_attention(a) -> dict:
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    dt = DT[a.dtype]
+    q = torch.randn((a.B, a.H, a.S, a.D), device=dev, generator=g).to(dt)
+    k = torch.randn((a.B, a.Hkv, a.S, a.D), device=dev, generator=g).to(dt)
+    v = torch.randn((a.B, a.Hkv, a.S, a.D), device=dev, generator=g).to(dt)
+    o = torch.empty((a.B, a.H, a.S, a.D), dtype=DT[a.odtype], device=dev)
+    cu = None
+    pairs = a.S * a.S
+    if a.segments:
+        cu_np = _segments(a.segments, a.S)
+        cu = torch.from_numpy(cu_np).to(dev)
+        L = np.diff(cu_np.astype(np.int64))
+        pairs = int(np.sum(L * (L + 1) // 2)) if a.causal else int(np.sum(L * L))
+    elif a.causal:
+        pairs = a.S * (a.S + 1) // 2
+    us = _time(lambda i: attention(q, k, v, out=o, is_causal=a.causal, cu_seqlens=cu), a.iters, a.warmup)
+    flops = 4.0 * a.B * a.H * a.D * pairs
+    return {"op": "attention", "B": a.B, "H": a.H, "Hkv": a.Hkv, "S": a.S, "D": a.D,
+            "dtype": a.dtype, "odtype": a.odtype, "causal": a.causal, "segments": a.segments,
+            "us": round(us, 3), "tflops": round(flops / us / 1e6, 2),
+            "frac_mfma_peak": round(flops / us / 1e6 / PEAK_TFLOPS, 4)}
+
+
+def bench_qk_prep(a) -> dict:
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    dt = DT[a.dtype]
+    q = torch.randn((1, a.S, a.Hq, a.D), device=dev, generator=g).to(dt)
+    k = torch.randn((1, a.S, a.Hkv, a.D), device=dev, generator=g).to(dt)
+    v = torch.randn((1, a.S, a.Hkv, a.D), device=dev, generator=g).to(dt)
+    nq = RmsNorm(torch.ones(a.D, device=dev))
+    nk = RmsNorm(torch.ones(a.D, device=dev))
+    cs = torch.rand((1, a.S, a.D), device=dev, generator=g)
+    sn = torch.rand((1, a.S, a.D), device=dev, generator=g)
+    us = _time(lambda i: qk_norm_rope(q, k, v, nq, nk, cs, sn), a.iters, a.warmup)
+    esz = {"f32": 4, "f16": 2, "bf16": 2}[a.dtype]
+    rows = a.S * (a.Hq + 2 * a.Hkv)
+    bytes_ = rows * a.D * (esz + 2) + 2 * a.S * a.D * 4
+    return {"op": "qk_prep", "S": a.S, "Hq": a.Hq, "Hkv": a.Hkv, "D": a.D, "dtype": a.dtype,
+            "us": round(us, 3), "gbs": round(bytes_ / us / 1e3, 1),
+            "frac_hbm_peak": round(bytes_ / us / 1e3 / PEAK_GBS, 4)}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(prog="python -m burn_image_amd.perf")
+    sub = ap.add_subparsers(dest="op", required=True)
+    p = sub.add_parser("q4_linear")
+    p.add_argument("--M", type=int, default=4608)
+    p.add_argument("--K", type=int, default=3072)
+    p.add_argument("--N", type=int, default=9216)
+    p.add_argument("--layout", type=int, default=1)
+    p.add_argument("--block", type=int, default=128)
+    p.add_argument("--xdtype", default="bf16", choices=list(DT))
+    p.add_argument("--ydtype", default="f32", choices=list(DT))
+    p.add_argument("--rotate-bytes", type=float, default=0.0)
+    p = sub.add_parser("attention")
+    p.add_argument("--B", type=int, default=1)
+    p.add_argument("--H", type=int, default=24)
+    p.add_argument("--Hkv", type=int, default=24)
+    p.add_argument("--S", type=int, default=4608)
+    p.add_argument("--D", type=int, default=128)
+    p.add_argument("--dtype", default="bf16", choices=list(DT))
+    p.add_argument("--odtype", default="f32", choices=list(DT))
+    p.add_argument("--causal", action="store_true")
+    p.add_argument("--segments", default="", help="total:min:max segment draw (as the C5 workload)")
+    p = sub.add_parser("qk_prep")
+    p.add_argument("--S", type=int, default=4608)
+    p.add_argument("--Hq", type=int, default=24)
+    p.add_argument("--Hkv", type=int, default=24)
+    p.add_argument("--D", type=int, default=128)
+    p.add_argument("--dtype", default="f32", choices=list(DT))
+    for p in sub.choices.values():
+        p.add_argument("--iters", type=int, default=50)
+        p.add_argument("--warmup", type=int, default=5)
+    a = ap.parse_args(argv)
+    _lib.load()
+    fn = {"q4_linear": bench_q4_linear, "attention": bench_attention, "qk_prep": bench_qk_prep}[a.op]
+    print(json.dumps(fn(a)), flush=True)
+
+
+if __name__ == "__main__":
+    sys.exit(main())
