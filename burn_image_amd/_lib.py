@@ -10,7 +10,8 @@ import os
 import threading
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "libbiq.so")
+# BIQ_LIBRARY selects another build of the same ABI (e.g. a tuning variant).
+LIB_PATH = os.environ.get("BIQ_LIBRARY") or os.path.join(PKG, "libbiq.so")
 
 OK = 0
 ERR_INVALID_ARG = 1

@@ -18,7 +18,8 @@
 //    so the f32 block scale is never rounded to 16 bits.
 //
 // Schedule: 512 threads = 8 waves (2 per SIMD) in a 2 (M) x 4 (N) grid; workgroup tile
-// 128 x 256, wave tile 64 x 64 (2 x 2 MFMA 32 x 32 tiles); K advances 64 per tile.  While the
+// 128 x 256, wave tile 64 x 64 (2 x 2 MFMA 32 x 32 tiles); K advances 128 per tile (64 for f32
+// activations).  While the
 // waves run the MFMAs of tile t from one LDS buffer, every thread already holds tile t+1's global
 // loads (activations, packed words and block scales) in registers; it converts and stores them
 // into the other LDS buffer afterwards, so one barrier per tile separates the two.  Workgroups are
@@ -28,10 +29,6 @@
 
 namespace {
 
-constexpr int BM = 128, BN = 256, BK = 64, NTHREADS = 512;
-constexpr int WAVES_N = 4;
-constexpr int A_LD = BK + 8;  // LDS row stride of the activation tile, in halves (16 B pad)
-constexpr int B_LD = BN;      // LDS row stride of the word tile, in words
 constexpr int GROUP_M = 8;    // M tiles per raster group
 
 enum XMode { XM_F16 = 0, XM_BF16 = 1, XM_F32 = 2 };
@@ -96,30 +93,54 @@ __device__ __forceinline__ float load_scale(const float *__restrict__ scales, in
   return LAYOUT == BIQ_Q4_KN_AXIS1 ? scales[b * N + n] : scales[n * nblk + b];
 }
 
-// Per-thread register copy of one tile's global data.
-template <int XMODE>
-struct TileRegs {
+// Tile geometry: a wave owns WM x WN MFMA tiles of 32 x 32; the workgroup holds WAVES_M x WAVES_N
+// waves.
+template <int WM_, int WN_, int WAVES_M_, int WAVES_N_, int BK_>
+struct Geo {
+  static constexpr int WM = WM_, WN = WN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr int BK = BK_;        // K per LDS stage
+  static constexpr int A_LD = BK + 8;   // LDS row stride of the activation tile, in halves
+  static constexpr int BM = 32 * WM * WAVES_M, BN = 32 * WN * WAVES_N;
+  static constexpr int NTHREADS = 64 * WAVES_M * WAVES_N;
   static constexpr int A_CHUNKS = (BM * BK / 8) / NTHREADS;  // 8-element groups per thread
-  u32x4_t a16[XMODE == XM_F32 ? 1 : A_CHUNKS];
-  float4 a32[XMODE == XM_F32 ? 2 * A_CHUNKS : 1];
-  u32x4_t b;
+  static constexpr int B_CHUNKS = (BK / 8) * (BN / 4) / NTHREADS;  // 4-word groups per thread
+  static_assert(A_CHUNKS * NTHREADS == BM * BK / 8, "activation tile split");
+  static_assert(B_CHUNKS * NTHREADS == (BK / 8) * (BN / 4), "word tile split");
 };
 
-template <int LAYOUT, int XMODE, int BLK>
-__global__ void __launch_bounds__(NTHREADS, 1)
+// Workgroup shape: 8 waves (2 per SIMD) in a 2 x 4 grid of 64 x 64 wave tiles -> 128 x 256.
+// 16-bit activations stage K 128 at a time (more bytes in flight per prefetch); the f32 hi/lo
+// path keeps 64 so that its two activation planes fit the 160 KB LDS, and blocks of 8 or 16 keep
+// 64 so that their per-tile scale lists stay in registers.
+template <int XMODE, int BLK>
+using GemmGeo = Geo<2, 2, 2, 4, (XMODE == XM_F32 || BLK <= 16) ? 64 : 128>;
+
+// Per-thread register copy of one tile's global data.
+template <class G, int XMODE>
+struct TileRegs {
+  u32x4_t a16[XMODE == XM_F32 ? 1 : G::A_CHUNKS];
+  float4 a32[XMODE == XM_F32 ? 2 * G::A_CHUNKS : 1];
+  u32x4_t b[G::B_CHUNKS];
+};
+
+template <class G, int LAYOUT, int XMODE, int BLK>
+__global__ void __launch_bounds__(G::NTHREADS, 1)
     q4_gemm_kernel(const void *__restrict__ xv, int64_t ldx, const uint32_t *__restrict__ words,
                    const float *__restrict__ scales, const float *__restrict__ bias,
                    void *__restrict__ yv, int y_dtype, int64_t M, int64_t N, int64_t K,
                    int tiles_m, int tiles_n) {
+  constexpr int WM = G::WM, WN = G::WN, BM = G::BM, BN = G::BN, NT = G::NTHREADS;
+  constexpr int BK = G::BK, A_LD = G::A_LD;
+  constexpr int B_LD = BN;  // LDS row stride of the word tile, in words
   constexpr int NSPLIT = XMODE == XM_F32 ? 2 : 1;
-  constexpr int A_CHUNKS = TileRegs<XMODE>::A_CHUNKS;
   constexpr int TILE_BLOCKS = BLK >= BK ? 1 : BK / BLK;
+  constexpr int TPB = BLK >= BK ? BLK / BK : 1;  // K tiles per outer iteration
   __shared__ __attribute__((aligned(16))) uint16_t As[2][NSPLIT][BM * A_LD];
   __shared__ __attribute__((aligned(16))) uint32_t Bs[2][(BK / 8) * B_LD];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
   const int l32 = lane & 31, lh = lane >> 5;
 
   // ---- XCD-aware, M-grouped tile order
@@ -139,16 +160,16 @@ __global__ void __launch_bounds__(NTHREADS, 1)
   const int64_t nblk = K / BLK;
   const int64_t KW = K / 8;
 
-  int64_t ncol[2];
+  int64_t ncol[WN];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) ncol[j] = n0 + wn * 64 + 32 * j + l32;
+  for (int j = 0; j < WN; ++j) ncol[j] = n0 + wn * (32 * WN) + 32 * j + l32;
 
   // ---- global -> registers for one K tile
-  auto load_tile = [&](int64_t kt, TileRegs<XMODE> &R, float (&sc)[2][TILE_BLOCKS]) {
+  auto load_tile = [&](int64_t kt, TileRegs<G, XMODE> &R, float (&sc)[WN][TILE_BLOCKS]) {
 #pragma unroll
-    for (int it = 0; it < A_CHUNKS; ++it) {
-      const int c = tid + it * NTHREADS;
-      const int row = c >> 3, kc = c & 7;
+    for (int it = 0; it < G::A_CHUNKS; ++it) {
+      const int c = tid + it * NT;
+      const int row = c / (BK / 8), kc = c % (BK / 8);
       const int64_t gm = m0 + row, gk = kt + 8 * kc;
       const bool ok = gm < M && gk < K;
       if constexpr (XMODE == XM_F32) {
@@ -163,40 +184,44 @@ __global__ void __launch_bounds__(NTHREADS, 1)
       }
     }
     const int64_t kw0 = kt / 8;
-    if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
-      const int kwr = tid >> 6, nc = (tid & 63) * 4;
-      R.b = (kw0 + kwr < KW && n0 + nc < N)
-                ? *reinterpret_cast<const u32x4_t *>(words + (kw0 + kwr) * N + n0 + nc)
-                : u32x4_t{0u, 0u, 0u, 0u};
-    } else {
-      const int nl = tid >> 1, half = tid & 1;
-      const int64_t n = n0 + nl, kwb = kw0 + 4 * half;
-      u32x4_t w = {0u, 0u, 0u, 0u};
-      if (n < N) {
-        const uint32_t *src = words + n * KW + kwb;
-        if ((KW & 3) == 0 && kwb + 3 < KW) {
-          w = *reinterpret_cast<const u32x4_t *>(src);
-        } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (kwb + j < KW) w[j] = src[j];
+    for (int it = 0; it < G::B_CHUNKS; ++it) {
+      const int c = tid + it * NT;
+      if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
+        const int kwr = c / (BN / 4), nc = (c % (BN / 4)) * 4;
+        R.b[it] = (kw0 + kwr < KW && n0 + nc < N)
+                      ? *reinterpret_cast<const u32x4_t *>(words + (kw0 + kwr) * N + n0 + nc)
+                      : u32x4_t{0u, 0u, 0u, 0u};
+      } else {
+        const int nl = c / (BK / 32), part4 = c % (BK / 32);
+        const int64_t n = n0 + nl, kwb = kw0 + 4 * part4;
+        u32x4_t w = {0u, 0u, 0u, 0u};
+        if (n < N) {
+          const uint32_t *src = words + n * KW + kwb;
+          if ((KW & 3) == 0 && kwb + 3 < KW) {
+            w = *reinterpret_cast<const u32x4_t *>(src);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (kwb + j < KW) w[j] = src[j];
+          }
         }
+        R.b[it] = w;
       }
-      R.b = w;
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int t = 0; t < TILE_BLOCKS; ++t)
         sc[j][t] = load_scale<LAYOUT>(scales, kt / BLK + t, ncol[j], N, nblk);
   };
 
   // ---- registers -> LDS buffer (activation conversion to f16 slot order happens here)
-  auto store_tile = [&](const TileRegs<XMODE> &R, int buf) {
+  auto store_tile = [&](const TileRegs<G, XMODE> &R, int buf) {
 #pragma unroll
-    for (int it = 0; it < A_CHUNKS; ++it) {
-      const int c = tid + it * NTHREADS;
-      const int row = c >> 3, kc = c & 7;
+    for (int it = 0; it < G::A_CHUNKS; ++it) {
+      const int c = tid + it * NT;
+      const int row = c / (BK / 8), kc = c % (BK / 8);
       u32x4_t hi, lo;
       if constexpr (XMODE == XM_BF16) hi = bf16x8_to_f16_slots(R.a16[it]);
       else if constexpr (XMODE == XM_F16) hi = f16x8_to_slots(R.a16[it]);
@@ -204,131 +229,148 @@ __global__ void __launch_bounds__(NTHREADS, 1)
       *reinterpret_cast<u32x4_t *>(&As[buf][0][row * A_LD + 8 * kc]) = hi;
       if constexpr (NSPLIT == 2) *reinterpret_cast<u32x4_t *>(&As[buf][1][row * A_LD + 8 * kc]) = lo;
     }
-    if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
-      const int kwr = tid >> 6, nc = (tid & 63) * 4;
-      *reinterpret_cast<u32x4_t *>(&Bs[buf][kwr * B_LD + nc]) = R.b;
-    } else {
-      const int nl = tid >> 1, half = tid & 1;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) Bs[buf][(4 * half + j) * B_LD + nl] = R.b[j];
+    for (int it = 0; it < G::B_CHUNKS; ++it) {
+      const int c = tid + it * NT;
+      if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
+        const int kwr = c / (BN / 4), nc = (c % (BN / 4)) * 4;
+        *reinterpret_cast<u32x4_t *>(&Bs[buf][kwr * B_LD + nc]) = R.b[it];
+      } else {
+        const int nl = c / (BK / 32), part4 = c % (BK / 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Bs[buf][(4 * part4 + j) * B_LD + nl] = R.b[it][j];
+      }
     }
   };
 
-  floatx16_t acc[2][2], part[2][2];
+  floatx16_t acc[WM][WN], part[WM][WN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      acc[i][j] = biq::zero16();
-      part[i][j] = biq::zero16();
-    }
+    for (int j = 0; j < WN; ++j) acc[i][j] = biq::zero16();
 
-  TileRegs<XMODE> R;
-  float sc[2][TILE_BLOCKS], sc_next[2][TILE_BLOCKS];
+  // LDS operand reads of one K16 step: WM activation fragments and WN packed words.
+  auto read_step = [&](int buf, int s, half8_t (&a)[WM][NSPLIT], uint32_t (&w)[WN]) {
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int x = 0; x < NSPLIT; ++x)
+        a[i][x] = *reinterpret_cast<const half8_t *>(
+            &As[buf][x][(wm * (32 * WM) + 32 * i + l32) * A_LD + 16 * s + 8 * lh]);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) w[j] = Bs[buf][(2 * s + lh) * B_LD + wn * (32 * WN) + 32 * j + l32];
+  };
+
+  // Pipeline: R holds tile t+1 while tile t computes; tile t+1 is stored into the other LDS
+  // buffer at the start of iteration t (its conversion overlaps the first LDS reads of tile t)
+  // and the loads of tile t+2 are issued right after, a whole tile ahead of their use.
+  TileRegs<G, XMODE> R;
+  float sc[WN][TILE_BLOCKS], sc_next[WN][TILE_BLOCKS];
   load_tile(0, R, sc);
   store_tile(R, 0);
+  if (BK < K) load_tile(BK, R, sc_next);
   __syncthreads();
 
   int buf = 0;
-  for (int64_t kt = 0; kt < K; kt += BK, buf ^= 1) {
-    const bool has_next = kt + BK < K;
-    if (has_next) load_tile(kt + BK, R, sc_next);
+  // Outer iterations cover whole quantisation blocks (or one K tile of several small blocks),
+  // so the first / last step of every block is known at compile time: the MFMA chain of a block
+  // starts from an inline zero and no accumulator is copied or selected at run time.
+  for (int64_t kg = 0; kg < K; kg += TPB * BK) {
+#pragma unroll
+    for (int tt = 0; tt < TPB; ++tt) {
+      const int64_t kt = kg + tt * BK;
+      const bool has_next = kt + BK < K;
 
-    // ---------------- MFMA over the 4 K16 steps of tile kt ---------------------------------
+      half8_t a_cur[WM][NSPLIT], a_nxt[WM][NSPLIT];
+      uint32_t w_cur[WN], w_nxt[WN];
+      half8_t b_cur[WN];
+      read_step(buf, 0, a_cur, w_cur);
+      float sc_cur[WN][TILE_BLOCKS];
 #pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      if (kt + 16 * s >= K) break;
-      half8_t a[2][NSPLIT];
+      for (int j = 0; j < WN; ++j)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int t = 0; t < TILE_BLOCKS; ++t) sc_cur[j][t] = sc[j][t];
+      if (has_next) {
+        store_tile(R, buf ^ 1);
 #pragma unroll
-        for (int x = 0; x < NSPLIT; ++x)
-          a[i][x] = *reinterpret_cast<const half8_t *>(
-              &As[buf][x][(wm * 64 + 32 * i + l32) * A_LD + 16 * s + 8 * lh]);
-      half8_t bq[2];
+        for (int j = 0; j < WN; ++j)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bq[j] = unpack_q4_f16(Bs[buf][(2 * s + lh) * B_LD + wn * 64 + 32 * j + l32]);
+          for (int t = 0; t < TILE_BLOCKS; ++t) sc[j][t] = sc_next[j][t];
+        if (kt + 2 * BK < K) load_tile(kt + 2 * BK, R, sc_next);
+      }
+#pragma unroll
+      for (int j = 0; j < WN; ++j) b_cur[j] = unpack_q4_f16(w_cur[j]);
 
-      if constexpr (BLK == 8) {
-        // Lanes 0-31 carry block 2g, lanes 32-63 block 2g + 1: two masked MFMAs.
-        const half8_t zh = {0, 0, 0, 0, 0, 0, 0, 0};
+      // A partial last tile (K % 64 != 0, small blocks only) runs to the end: its activations,
+      // words and scales beyond K were loaded as zeros, so the extra steps add exact zeros.
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const half8_t b_lo = lh == 0 ? bq[j] : zh;
-          const half8_t b_hi = lh == 0 ? zh : bq[j];
+      for (int s = 0; s < BK / 16; ++s) {
+        if (s + 1 < BK / 16) read_step(buf, s + 1, a_nxt, w_nxt);
+
+        if constexpr (BLK == 8) {
+          // Lanes 0-31 carry block 2g, lanes 32-63 block 2g + 1: two masked MFMAs.
+          const half8_t zh = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            floatx16_t p = biq::mfma32x32x16_f16(a[i][0], b_lo, biq::zero16());
-            if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a[i][1], b_lo, p);
-            acc[i][j] += sc[j][2 * s] * p;
-            p = biq::mfma32x32x16_f16(a[i][0], b_hi, biq::zero16());
-            if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a[i][1], b_hi, p);
-            acc[i][j] += sc[j][2 * s + 1] * p;
+          for (int j = 0; j < WN; ++j) {
+            const half8_t b_lo = lh == 0 ? b_cur[j] : zh;
+            const half8_t b_hi = lh == 0 ? zh : b_cur[j];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) {
+              floatx16_t p = biq::mfma32x32x16_f16(a_cur[i][0], b_lo, biq::zero16());
+              if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a_cur[i][1], b_lo, p);
+              acc[i][j] += sc_cur[j][2 * s] * p;
+              p = biq::mfma32x32x16_f16(a_cur[i][0], b_hi, biq::zero16());
+              if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a_cur[i][1], b_hi, p);
+              acc[i][j] += sc_cur[j][2 * s + 1] * p;
+            }
+          }
+        } else {
+          constexpr int SPB = BLK / 16;  // K16 steps per block
+          const bool first = BLK >= BK ? (tt == 0 && s == 0) : (s % SPB) == 0;
+          const bool last = BLK >= BK ? (tt == TPB - 1 && s == BK / 16 - 1) : (s % SPB) == SPB - 1;
+          const int tb = BLK >= BK ? 0 : s / SPB;
+#pragma unroll
+          for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+              floatx16_t p =
+                  biq::mfma32x32x16_f16(a_cur[i][0], b_cur[j], first ? biq::zero16() : part[i][j]);
+              if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a_cur[i][1], b_cur[j], p);
+              part[i][j] = p;
+            }
+          if (last) {
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+              for (int j = 0; j < WN; ++j) acc[i][j] += sc_cur[j][tb] * part[i][j];
           }
         }
-      } else {
-        constexpr int SPB = BLK / 16;  // K16 steps per block
-        bool first, last;
-        int tb;
-        if constexpr (BLK >= BK) {
-          first = (s == 0) && (kt % BLK == 0);
-          last = (s == BK / 16 - 1) && ((kt + BK) % BLK == 0);
-          tb = 0;
-        } else {
-          first = (s % SPB) == 0;
-          last = (s % SPB) == SPB - 1;
-          tb = s / SPB;
-        }
-        if (first) {
+
+        if (s + 1 < BK / 16) {
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
+          for (int j = 0; j < WN; ++j) b_cur[j] = unpack_q4_f16(w_nxt[j]);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              floatx16_t p = biq::mfma32x32x16_f16(a[i][0], bq[j], biq::zero16());
-              if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a[i][1], bq[j], p);
-              part[i][j] = p;
-            }
-        } else {
+          for (int i = 0; i < WM; ++i)
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              floatx16_t p = biq::mfma32x32x16_f16(a[i][0], bq[j], part[i][j]);
-              if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a[i][1], bq[j], p);
-              part[i][j] = p;
-            }
-        }
-        if (last) {
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] += sc[j][tb] * part[i][j];
+            for (int x = 0; x < NSPLIT; ++x) a_cur[i][x] = a_nxt[i][x];
         }
       }
+      __syncthreads();
+      buf ^= 1;
     }
-
-    if (has_next) {
-      store_tile(R, buf ^ 1);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int t = 0; t < TILE_BLOCKS; ++t) sc[j][t] = sc_next[j][t];
-    }
-    __syncthreads();
   }
 
   // ---------------- epilogue: bias, convert, store ------------------------------------------
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < WN; ++j) {
     const int64_t col = ncol[j];
     if (col >= N) continue;
     const float bv = bias ? bias[col] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+        const int64_t row = m0 + wm * (32 * WM) + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (row >= M) continue;
         const float v = acc[i][j][r] + bv;
         if (y_dtype == BIQ_DTYPE_F32) {
@@ -346,15 +388,24 @@ template <int LAYOUT, int XMODE>
 int launch_blk(hipStream_t s, int block, const void *x, int64_t ldx, const uint32_t *words,
                const float *scales, const float *bias, void *y, int y_dtype, int64_t M, int64_t N,
                int64_t K) {
-  const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
+  using G8 = GemmGeo<XMODE, 8>;
+  using G16 = GemmGeo<XMODE, 16>;
+  using G = GemmGeo<XMODE, 128>;
+  const int tiles_m = (int)((M + G::BM - 1) / G::BM), tiles_n = (int)((N + G::BN - 1) / G::BN);
   dim3 grid((unsigned)((int64_t)tiles_m * tiles_n));
-  dim3 blk(NTHREADS);
+  dim3 blk(G::NTHREADS);
 #define BIQ_LAUNCH(B)                                                                              \
-  hipLaunchKernelGGL((q4_gemm_kernel<LAYOUT, XMODE, B>), grid, blk, 0, s, x, ldx, words, scales,  \
-                     bias, y, y_dtype, M, N, K, tiles_m, tiles_n)
+  hipLaunchKernelGGL((q4_gemm_kernel<G, LAYOUT, XMODE, B>), grid, blk, 0, s, x, ldx, words,       \
+                     scales, bias, y, y_dtype, M, N, K, tiles_m, tiles_n)
   switch (block) {
-    case 8: BIQ_LAUNCH(8); break;
-    case 16: BIQ_LAUNCH(16); break;
+    case 8:
+      hipLaunchKernelGGL((q4_gemm_kernel<G8, LAYOUT, XMODE, 8>), grid, blk, 0, s, x, ldx, words,
+                         scales, bias, y, y_dtype, M, N, K, tiles_m, tiles_n);
+      break;
+    case 16:
+      hipLaunchKernelGGL((q4_gemm_kernel<G16, LAYOUT, XMODE, 16>), grid, blk, 0, s, x, ldx, words,
+                         scales, bias, y, y_dtype, M, N, K, tiles_m, tiles_n);
+      break;
     case 32: BIQ_LAUNCH(32); break;
     case 64: BIQ_LAUNCH(64); break;
     default: BIQ_LAUNCH(128); break;
@@ -402,7 +453,7 @@ extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M
       (reinterpret_cast<uintptr_t>(words) & 15) || (reinterpret_cast<uintptr_t>(scales) & 3))
     return biq::fail(BIQ_ERR_INVALID_ARG,
                      "q4 linear requires 16-byte aligned activation rows and packed words");
-  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const int64_t tiles = ((M + 127) / 128) * ((N + 255) / 256);
   if (tiles > 0x7fffffffLL)
     return biq::fail(BIQ_ERR_UNSUPPORTED, "q4 linear output has too many tiles for one launch");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
