@@ -3,7 +3,10 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 
 #include "common.h"
 
@@ -22,6 +25,34 @@ int check_launch(const char *what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return fail(BIQ_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+  return BIQ_OK;
+}
+
+// One grow-only scratch buffer per (device, stream): calls on one stream run in order, so they
+// may share it; calls on different streams never do.  A buffer that is outgrown is kept, not
+// freed (a captured graph may still name it); all of them live until the process ends.
+static std::mutex g_ws_mutex;
+static std::map<std::pair<int, uintptr_t>, std::pair<void *, size_t>> g_ws;
+
+int stream_workspace(hipStream_t s, size_t bytes, void **out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(BIQ_ERR_HIP, "workspace: no current device");
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  auto &e = g_ws[{dev, reinterpret_cast<uintptr_t>(s)}];
+  if (e.first != nullptr && e.second >= bytes) {
+    *out = e.first;
+    return BIQ_OK;
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return fail(BIQ_ERR_UNSUPPORTED,
+                "split-K workspace must grow outside stream capture: make the same call once before capturing");
+  size_t want = bytes > 2 * e.second ? bytes : 2 * e.second;
+  want = (want + (1u << 20) - 1) & ~((size_t)(1u << 20) - 1);
+  void *p = nullptr;
+  if (hipMalloc(&p, want) != hipSuccess) return fail(BIQ_ERR_HIP, "workspace: hipMalloc failed");
+  e = {p, want};
+  *out = p;
   return BIQ_OK;
 }
 

@@ -30,6 +30,8 @@ void clear_error();
 int fail(int status, const std::string &msg);
 // Check the launch status of the last kernel on this thread.
 int check_launch(const char *what);
+// Device scratch owned by the library for (current device, stream s), at least `bytes` long.
+int stream_workspace(hipStream_t s, size_t bytes, void **out);
 
 // ---------------------------------------------------------------------------------------------
 // device helpers

@@ -112,8 +112,11 @@ struct Geo {
 // 16-bit activations stage K 128 at a time (more bytes in flight per prefetch); the f32 hi/lo
 // path keeps 64 so that its two activation planes fit the 160 KB LDS, and blocks of 8 or 16 keep
 // 64 so that their per-tile scale lists stay in registers.
+#ifndef BIQ_GEMM_WAVES
+#define BIQ_GEMM_WAVES 2, 2, 2, 4
+#endif
 template <int XMODE, int BLK>
-using GemmGeo = Geo<2, 2, 2, 4, (XMODE == XM_F32 || BLK <= 16) ? 64 : 128>;
+using GemmGeo = Geo<BIQ_GEMM_WAVES, (XMODE == XM_F32 || BLK <= 16) ? 64 : 128>;
 
 // Per-thread register copy of one tile's global data.
 template <class G, int XMODE>
@@ -430,6 +433,12 @@ int launch_layout(hipStream_t s, int x_dtype, int block, const void *x, int64_t 
 
 }  // namespace
 
+namespace biq {
+int q4_gemv_launch(hipStream_t s, const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                   const uint32_t *words, const float *scales, int layout, int block, int64_t N,
+                   const float *bias, float *y);
+}
+
 extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K,
                              int64_t ldx, const uint32_t *words, const float *scales, int layout,
                              int block, int64_t N, const float *bias, void *y, int y_dtype) {
@@ -453,10 +462,16 @@ extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M
       (reinterpret_cast<uintptr_t>(words) & 15) || (reinterpret_cast<uintptr_t>(scales) & 3))
     return biq::fail(BIQ_ERR_INVALID_ARG,
                      "q4 linear requires 16-byte aligned activation rows and packed words");
-  const int64_t tiles = ((M + 127) / 128) * ((N + 255) / 256);
+  using G0 = GemmGeo<BIQ_DTYPE_BF16, 128>;
+  const int64_t tiles = ((M + G0::BM - 1) / G0::BM) * ((N + G0::BN - 1) / G0::BN);
   if (tiles > 0x7fffffffLL)
     return biq::fail(BIQ_ERR_UNSUPPORTED, "q4 linear output has too many tiles for one launch");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Up to 16 rows with an f32 output stream the weights through the small-M kernel
+  // (q4_gemv.hip): split-K over the whole chip instead of N / 256 workgroups of 128 rows.
+  if (M <= 16 && y_dtype == BIQ_DTYPE_F32)
+    return biq::q4_gemv_launch(s, x, x_dtype, M, K, ldx, words, scales, layout, block, N, bias,
+                               reinterpret_cast<float *>(y));
   if (layout == BIQ_Q4_KN_AXIS1)
     return launch_layout<BIQ_Q4_KN_AXIS1>(s, x_dtype, block, x, ldx, words, scales, bias, y, y_dtype,
                                           M, N, K);

@@ -5,6 +5,7 @@
     python -m burn_image_amd.perf attention --B 1 --H 24 --Hkv 24 --S 4608 --D 128 [--dtype bf16]
                                             [--causal] [--segments 1024:64:512]
     python -m burn_image_amd.perf qk_prep --S 4608 --Hq 24 --Hkv 24 --D 128 [--dtype f32]
+    (every op also takes --iters, --warmup and --graph)
 
 Inputs are random and resident on the GPU before timing; weights rotate over enough distinct
 copies (``--rotate-bytes``, default 0) to defeat the 256 MB MALL when measuring HBM-bound shapes.
@@ -28,15 +29,36 @@ PEAK_TFLOPS = 2500.0
 PEAK_GBS = 8000.0
 
 
+_GRAPH = False
+
+
 def _time(fn, iters: int, warmup: int) -> float:
+    """Average microseconds per call.  With --graph the `iters` calls are captured once in a HIP
+    graph and replayed, so short kernels are timed without the host's per-call cost between
+    them (every call here writes a preallocated output and allocates nothing)."""
     for _ in range(warmup):
         fn(0)
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for i in range(iters):
-        fn(i)
-    e.record()
+    if _GRAPH:
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):  # per-stream library state (workspace) is sized here
+            fn(0)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(iters):
+                fn(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        s.record()
+        graph.replay()
+        e.record()
+    else:
+        s.record()
+        for i in range(iters):
+            fn(i)
+        e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / iters * 1e3  # microseconds
 
@@ -148,7 +170,10 @@ def main(argv=None):
     for p in sub.choices.values():
         p.add_argument("--iters", type=int, default=50)
         p.add_argument("--warmup", type=int, default=5)
+        p.add_argument("--graph", action="store_true", help="replay the calls from a HIP graph")
     a = ap.parse_args(argv)
+    global _GRAPH
+    _GRAPH = a.graph
     _lib.load()
     fn = {"q4_linear": bench_q4_linear, "attention": bench_attention, "qk_prep": bench_qk_prep}[a.op]
     print(json.dumps(fn(a)), flush=True)

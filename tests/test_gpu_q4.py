@@ -181,3 +181,79 @@ def test_gpu_real_checkpoint_shapes(gpu, oracle):
         y = host(B.q_matmul(dev(x, device=gpu), q))
         ref = oracle.q4_linear_f64(x, words, scales, 1, blk, N).astype(np.float32)
         assert_parity(y, ref, f"real_{K}x{N}_blk{blk}")
+
+
+@pytest.mark.parametrize("layout", [1, 0])
+@pytest.mark.parametrize("block", [8, 16, 32, 64, 128])
+@pytest.mark.parametrize("xdt", ["bf16", "f32", "f16"])
+@pytest.mark.parametrize("M", [1, 7, 16])
+def test_gpu_q4_linear_small_m(gpu, oracle, layout, block, xdt, M):
+    """Rows <= 16 with an f32 output take the split-K streaming route: column tail (N = 200),
+    a K that is a multiple of 8 but not of 32 (block 8), and several K chunks per column group."""
+    K, N = (1048 if block == 8 else 1024), 200
+    x = W.activations(15, M + block, M, K, xdt)
+    words, scales = W.q4_weight(15, 3 + block + layout, K, N, layout=layout, block=block)
+    q = weight(words, scales, layout, block, K, N, gpu)
+    y = host(B.q_matmul(dev(x, TORCH_DT[xdt], gpu), q))
+    ref = oracle.q4_linear_f64(x, words, scales, layout, block, N).astype(np.float32)
+    assert_parity(y, ref, f"smallm_M{M}_blk{block}_l{layout}_{xdt}")
+
+
+def test_gpu_q4_linear_small_m_bias_and_boundary(gpu, oracle):
+    """Bias on the streaming route; M = 16 (streaming) and M = 17 (tiled MFMA route) agree with
+    the oracle on the same rows; a second call overwrites (the route accumulates atomically into
+    an output it first fills with the bias)."""
+    K, N = 3360, 840
+    blk = oracle.q4_kn_block(K, N)
+    x = W.activations(16, 1, 17, K, "bf16")
+    words, scales = W.q4_weight(16, 2, K, N, layout=1, block=blk)
+    bias = np.linspace(-1, 1, N).astype(np.float32)
+    lin = B.Linear(weight(words, scales, 1, blk, K, N, gpu), dev(bias, device=gpu))
+    ref = oracle.q4_linear_f64(x, words, scales, 1, blk, N, bias=bias).astype(np.float32)
+    xd = dev(x, torch.bfloat16, gpu)
+    out = torch.full((16, N), 123.0, device=gpu)
+    for _ in range(2):
+        B.q_matmul(xd[:16], lin.weight, out=out, bias=lin.bias)
+        assert_parity(host(out), ref[:16], "smallm_bias_M16")
+    assert_parity(host(B.linear_forward(lin, xd)), ref, "tiled_bias_M17")
+
+
+def test_gpu_q4_linear_modulation_row(gpu, oracle):
+    """One conditioning row through the released Boogu modulation width (3360 -> 4 x 3360)."""
+    K, N = 3360, 13440
+    blk = oracle.q4_kn_block(K, N)
+    x = W.activations(17, 1, 1, K, "f32")
+    words, scales = W.q4_weight(17, 2, K, N, layout=1, block=blk)
+    y = host(B.q_matmul(dev(x, device=gpu), weight(words, scales, 1, blk, K, N, gpu)))
+    ref = oracle.q4_linear_f64(x, words, scales, 1, blk, N).astype(np.float32)
+    assert_parity(y, ref, f"modulation_1x{K}x{N}_blk{blk}")
+
+
+def test_gpu_q4_linear_small_m_deterministic_and_graph_replay(gpu, oracle):
+    """Split-K partials are added in a fixed order: repeated calls are bitwise equal.  After one
+    eager call has sized the stream's workspace, the call can be captured in a HIP graph; every
+    replay (with eager work in between) matches the eager result bitwise."""
+    K, N, M = 3072, 1024, 3
+    x = W.activations(18, 1, M, K, "bf16")
+    words, scales = W.q4_weight(18, 2, K, N, layout=1)
+    q = weight(words, scales, 1, 128, K, N, gpu)
+    xd = dev(x, torch.bfloat16, gpu)
+    y0 = B.q_matmul(xd, q)
+    ref = oracle.q4_linear_f64(x, words, scales, 1, 128, N).astype(np.float32)
+    assert_parity(host(y0), ref, "smallm_det")
+    for _ in range(3):
+        assert torch.equal(B.q_matmul(xd, q), y0)
+    stream = torch.cuda.Stream()
+    out = torch.zeros((M, N), device=gpu)
+    with torch.cuda.stream(stream):
+        B.q_matmul(xd, q, out=out)  # sizes this stream's workspace outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        B.q_matmul(xd, q, out=out)
+    for i in range(4):
+        out.fill_(float(i))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y0), f"replay {i}"
+        B.q_matmul(xd[:1], q)  # unrelated eager work between replays
