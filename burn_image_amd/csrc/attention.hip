@@ -36,7 +36,7 @@ struct AttnArgs {
   const void *q, *k, *v;
   void *o;
   int64_t qs[3], ks[3], vs[3], os[3];  // batch, head, seq element strides
-  int64_t Hq, Hkv, Sq, Skv, D;
+  int64_t B, Hq, Hkv, Sq, Skv, D;
   float scale_log2;  // softmax scale * log2(e)
   int out_dtype;
   const int32_t *cu;
@@ -105,9 +105,20 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lh = lane >> 5;
-  const int64_t h = blockIdx.y, b = blockIdx.z;
+  // ---- XCD-aware order: the hardware places workgroup i on XCD i % 8; give each XCD a
+  //      contiguous run of (batch, head, query block) items, query blocks fastest, so the
+  //      workgroups sharing one head's K/V also share one XCD's L2.
+  int64_t h, b, qblk;
+  {
+    const int64_t nqb = (p.Sq + BQ - 1) / BQ;
+    const int64_t T = nqb * p.Hq * p.B, L = blockIdx.x;
+    const int64_t q8 = T / 8, r8 = T % 8, xcd = L % 8, slot = L / 8;
+    const int64_t pid = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + slot;
+    qblk = (pid % nqb) * BQ;
+    h = (pid / nqb) % p.Hq;
+    b = pid / (nqb * p.Hq);
+  }
   const int64_t hk = h / (p.Hq / p.Hkv);
-  const int64_t qblk = (int64_t)blockIdx.x * BQ;
   const int64_t qi = qblk + wave * 32 + l32;  // this lane's query row
   const int64_t D = p.D;
 
@@ -143,37 +154,70 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
     kv_end = kv_end < qlast + 1 ? kv_end : qlast + 1;
   }
   kv_begin = (kv_begin / BKV) * BKV;
-  const int64_t qmin = qblk + wave * 32, qmax = qmin + 31;  // this wave's query rows
-
-  // ---- global -> registers for the tile at kv0
-  auto load_tile = [&](int64_t kv0, KVRegs<DP, InT> &R) {
+  const int64_t qmin = qblk + wave * 32;  // this wave's first query row
+  // Visible keys of this lane: [vis_lo, vis_hi) (segment and causal bounds, capped at Skv).  A
+  // tile needs the mask unless it lies inside every lane's range of this wave.
+  int64_t vis_lo = seg_lo, vis_hi = seg_hi < p.Skv ? seg_hi : p.Skv;
+  if constexpr (MASK & MASK_CAUSAL) vis_hi = vis_hi < qi + 1 ? vis_hi : qi + 1;
+  int64_t wave_lo = vis_lo, wave_hi = vis_hi;
+  if constexpr (MASK != MASK_NONE) {
 #pragma unroll
-    for (int it = 0; it < K_CHUNKS; ++it) {
-      const int c = tid + it * NTHREADS;
-      const int row = c / (DP / 8), d0 = 8 * (c % (DP / 8));
-      const int64_t key = kv0 + row;
-      const bool ok = key < p.Skv && d0 < D;
-      if constexpr (F32IN)
-        R.k16[it] = ok ? load8_f32_as_f16(reinterpret_cast<const float *>(kg + key * p.ks[2] + d0))
-                       : u32x4_t{0u, 0u, 0u, 0u};
-      else
-        R.k16[it] = ok ? *reinterpret_cast<const u32x4_t *>(kg + key * p.ks[2] + d0)
-                       : u32x4_t{0u, 0u, 0u, 0u};
+    for (int sh = 1; sh < 64; sh <<= 1) {
+      const int64_t a = __shfl_xor(wave_lo, sh), c = __shfl_xor(wave_hi, sh);
+      wave_lo = a > wave_lo ? a : wave_lo;  // largest lower bound
+      wave_hi = c < wave_hi ? c : wave_hi;  // smallest upper bound
     }
+  }
+
+  // ---- global -> registers for the tile at kv0, through buffer loads.  The descriptor starts
+  //      at the tile's first key and ends at key Skv, so rows past the sequence read as zero
+  //      without a compare; chunks past the head width D get an offset beyond any range.  The
+  //      per-thread offsets stay fixed; only the (scalar) descriptor moves from tile to tile.
+  constexpr uint32_t OOB = 0x80000000u;
+  constexpr int64_t ESZ = sizeof(InT);
+  const int64_t krow_b = p.ks[2] * ESZ, vrow_b = p.vs[2] * ESZ;
+  uint32_t koff[K_CHUNKS], voff[4];
+#pragma unroll
+  for (int it = 0; it < K_CHUNKS; ++it) {
+    const int c = tid + it * NTHREADS;
+    const int row = c / (DP / 8), d0 = 8 * (c % (DP / 8));
+    koff[it] = d0 < D ? (uint32_t)(row * krow_b + d0 * ESZ) : OOB;
+  }
+  {
+    const int kb = tid % (BKV / 4), d0 = 8 * (tid / (BKV / 4));
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      voff[j] = (tid < V_GROUPS && d0 < D) ? (uint32_t)((4 * kb + j) * vrow_b + d0 * ESZ) : OOB;
+  }
+  auto rsrc = [&](const InT *base, int64_t kv0, int64_t row_b) {
+    // valid offsets stay below 2^31 (host check), so capping the range there keeps OOB
+    // offsets out of range for any sequence length
+    const int64_t rem = (p.Skv - kv0) * row_b;
+    const uint32_t n = rem > 0x7fffffffLL ? 0x7fffffffu : (uint32_t)rem;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<InT *>(base + kv0 * (row_b / ESZ)), 0,
+                                             (int)n, 0x00020000);
+  };
+  auto load16 = [&](const __amdgpu_buffer_rsrc_t &r, uint32_t off) -> u32x4_t {
+    if constexpr (F32IN) {
+      const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+      const u32x4_t b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0);
+      return u32x4_t{biq::pack_f16x2(biq::bitcast<float>(a[0]), biq::bitcast<float>(a[1])),
+                     biq::pack_f16x2(biq::bitcast<float>(a[2]), biq::bitcast<float>(a[3])),
+                     biq::pack_f16x2(biq::bitcast<float>(b[0]), biq::bitcast<float>(b[1])),
+                     biq::pack_f16x2(biq::bitcast<float>(b[2]), biq::bitcast<float>(b[3]))};
+    } else {
+      return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    }
+  };
+  auto load_tile = [&](int64_t kv0, KVRegs<DP, InT> &R) {
+    const auto rk = rsrc(kg, kv0, krow_b);
+#pragma unroll
+    for (int it = 0; it < K_CHUNKS; ++it) R.k16[it] = load16(rk, koff[it]);
     // V: thread owns keys 4 kb .. 4 kb + 3 at dims d0 .. d0 + 7 (key-consecutive lanes)
     if (tid < V_GROUPS) {
-      const int kb = tid % (BKV / 4), d0 = 8 * (tid / (BKV / 4));
+      const auto rv = rsrc(vg, kv0, vrow_b);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t key = kv0 + 4 * kb + j;
-        const bool ok = key < p.Skv && d0 < D;
-        if constexpr (F32IN)
-          R.v16[j] = ok ? load8_f32_as_f16(reinterpret_cast<const float *>(vg + key * p.vs[2] + d0))
-                        : u32x4_t{0u, 0u, 0u, 0u};
-        else
-          R.v16[j] = ok ? *reinterpret_cast<const u32x4_t *>(vg + key * p.vs[2] + d0)
-                        : u32x4_t{0u, 0u, 0u, 0u};
-      }
+      for (int j = 0; j < 4; ++j) R.v16[j] = load16(rv, voff[j]);
     }
   };
 
@@ -187,28 +231,25 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
     }
     if (tid < V_GROUPS) {
       const int kb = tid % (BKV / 4), d0 = 8 * (tid / (BKV / 4));
-      // f16 values v[j][e] of key 4 kb + j, dim d0 + e
-      _Float16 vv[4][8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t w = R.v16[j][i];
-          if constexpr (BF16) {
-            vv[j][2 * i] = (_Float16)biq::bf16_lo_to_f32(w);
-            vv[j][2 * i + 1] = (_Float16)biq::bf16_hi_to_f32(w);
-          } else {
-            vv[j][2 * i] = biq::bitcast<_Float16>((uint16_t)(w & 0xffffu));
-            vv[j][2 * i + 1] = biq::bitcast<_Float16>((uint16_t)(w >> 16));
-          }
-        }
-      }
+      // dim d0 + e of keys (j, j + 1) as one f16 pair: bf16 pairs convert two at a time, f16
+      // pairs are a byte permute of the two source words
       const int slot = vt_slot(4 * kb);  // the 4 keys keep consecutive slots
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        half2_t lo = {vv[0][e], vv[1][e]}, hi = {vv[2][e], vv[3][e]};
-        uint2 w = make_uint2(biq::bitcast<uint32_t>(lo), biq::bitcast<uint32_t>(hi));
-        *reinterpret_cast<uint2 *>(&Vt[buf][(d0 + e) * VT_LD + slot]) = w;
+        uint32_t pr[2];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const uint32_t w0 = R.v16[2 * h2][e / 2], w1 = R.v16[2 * h2 + 1][e / 2];
+          if constexpr (BF16) {
+            const float f0 = (e & 1) ? biq::bf16_hi_to_f32(w0) : biq::bf16_lo_to_f32(w0);
+            const float f1 = (e & 1) ? biq::bf16_hi_to_f32(w1) : biq::bf16_lo_to_f32(w1);
+            pr[h2] = biq::pack_f16x2(f0, f1);
+          } else {
+            // bytes of (w0, w1): the low halves are bytes 0-1 / 4-5, the high halves 2-3 / 6-7
+            pr[h2] = __builtin_amdgcn_perm(w1, w0, (e & 1) ? 0x07060302u : 0x05040100u);
+          }
+        }
+        *reinterpret_cast<uint2 *>(&Vt[buf][(d0 + e) * VT_LD + slot]) = make_uint2(pr[0], pr[1]);
       }
     }
   };
@@ -249,36 +290,32 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
       sacc[ks] = a;
     }
 
-    // ---- scale (log2 domain), mask where the tile needs it, row max
-    bool need_mask = kv0 + BKV > p.Skv;
-    if constexpr (MASK & MASK_SEGMENT) need_mask = true;
-    if constexpr (MASK & MASK_CAUSAL) need_mask = need_mask || (kv0 + BKV - 1 > qmin);
+    // ---- mask where the tile needs it; row max of the raw scores (the positive scale commutes
+    //      with max, so it is applied once to the maximum and folded into the exponent's FMA)
+    const bool need_mask = kv0 < wave_lo || kv0 + BKV > wave_hi;
     float mx = -INFINITY;
     if (need_mask) {
+      // key offsets inside the tile are small: compare in 32 bits against this lane's bounds,
+      // shifted by the lane's own key offset 4 lh
+      const int64_t lo64 = vis_lo - kv0 - 4 * lh, hi64 = vis_hi - kv0 - 4 * lh;
+      const int lo = lo64 < -BKV ? -BKV : (lo64 > 2 * BKV ? 2 * BKV : (int)lo64);
+      const int hi = hi64 > 2 * BKV ? 2 * BKV : (hi64 < -BKV ? -BKV : (int)hi64);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t key = kv0 + 32 * ks + 8 * (r >> 2) + 4 * lh + (r & 3);
-          bool ok = key < p.Skv;
-          if constexpr (MASK & MASK_SEGMENT) ok = ok && key >= seg_lo && key < seg_hi;
-          if constexpr (MASK & MASK_CAUSAL) ok = ok && key <= qi;
-          const float x = ok ? sacc[ks][r] * p.scale_log2 : -INFINITY;
-          sacc[ks][r] = x;
-          mx = fmaxf(mx, x);
+          const int kr = 32 * ks + 8 * (r >> 2) + (r & 3);  // key offset without 4 lh
+          const bool ok = kr >= lo && kr < hi;
+          sacc[ks][r] = ok ? sacc[ks][r] : -INFINITY;
+          mx = fmaxf(mx, sacc[ks][r]);
         }
     } else {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float x = sacc[ks][r] * p.scale_log2;
-          sacc[ks][r] = x;
-          mx = fmaxf(mx, x);
-        }
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[ks][r]);
     }
-    (void)qmax;
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * p.scale_log2;  // log2 domain
     // ---- move the reference maximum only when it grows by more than 2^8 (exact: O and l
     //      are both relative to the same reference)
     const bool grow = mx > m_run + 8.0f;
@@ -291,7 +328,10 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
 #pragma unroll
       for (int i = 0; i < DP / 32; ++i) oacc[i] *= alpha;
     }
-    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    const float neg_m = m_run == -INFINITY ? 0.0f : -m_run;
+    // p = 2^(s * scale_log2 - m) with one FMA; the row sum adds the f16-rounded p (the values
+    // the P V product uses) with v_dot2 against ones, two per instruction into f32
+    const half2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
     float rs = 0.0f;
     u32x4_t pf[4];  // P^T as f16 B operands of the four 16-key steps
 #pragma unroll
@@ -300,10 +340,11 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float e0 = __builtin_amdgcn_exp2f(sacc[ks][8 * t + 2 * j] - m_use);
-          const float e1 = __builtin_amdgcn_exp2f(sacc[ks][8 * t + 2 * j + 1] - m_use);
-          rs += e0 + e1;
-          pf[2 * ks + t][j] = biq::pack_f16x2(e0, e1);
+          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[ks][8 * t + 2 * j], p.scale_log2, neg_m));
+          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[ks][8 * t + 2 * j + 1], p.scale_log2, neg_m));
+          const uint32_t pk = biq::pack_f16x2(e0, e1);
+          pf[2 * ks + t][j] = pk;
+          rs = __builtin_amdgcn_fdot2(biq::bitcast<half2_t>(pk), ones, rs, false);
         }
     l_run += rs;
 
@@ -422,7 +463,9 @@ extern "C" int biq_attention(void *stream, const void *q, const void *k, const v
   for (int j = 0; j < 3; ++j)
     if (((o_strides[j] * osz) & 15) != 0)
       return biq::fail(BIQ_ERR_INVALID_ARG, "attention output strides must be multiples of 16 bytes");
-  if (B > 65535 || Hq > 65535 || (Sq + BQ - 1) / BQ > 0x7fffffff)
+  if (k_strides[2] * esz * BKV >= (1LL << 31) || v_strides[2] * esz * BKV >= (1LL << 31))
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "attention key/value row stride too large for 32-bit tile offsets");
+  if ((Sq + BQ - 1) / BQ * Hq * B > 0x7fffffffLL)
     return biq::fail(BIQ_ERR_UNSUPPORTED, "attention grid too large");
 
   AttnArgs a;
@@ -430,14 +473,14 @@ extern "C" int biq_attention(void *stream, const void *q, const void *k, const v
   for (int j = 0; j < 3; ++j) {
     a.qs[j] = q_strides[j]; a.ks[j] = k_strides[j]; a.vs[j] = v_strides[j]; a.os[j] = o_strides[j];
   }
-  a.Hq = Hq; a.Hkv = Hkv; a.Sq = Sq; a.Skv = Skv; a.D = D;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.Sq = Sq; a.Skv = Skv; a.D = D;
   const double sc = scale > 0.0f ? (double)scale : 1.0 / sqrt((double)D);
   a.scale_log2 = (float)(sc * 1.4426950408889634);
   a.out_dtype = out_dtype;
   a.cu = cu_seqlens;
   a.nseg = nseg;
   const int mask = (causal ? MASK_CAUSAL : 0) | (cu_seqlens ? MASK_SEGMENT : 0);
-  dim3 grid((unsigned)((Sq + BQ - 1) / BQ), (unsigned)Hq, (unsigned)B);
+  dim3 grid((unsigned)((Sq + BQ - 1) / BQ * Hq * B));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (D <= 64) launch_dtype<64>(s, grid, a, in_dtype, mask);
   else launch_dtype<128>(s, grid, a, in_dtype, mask);

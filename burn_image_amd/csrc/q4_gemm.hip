@@ -34,17 +34,25 @@ constexpr int GROUP_M = 8;    // M tiles per raster group
 enum XMode { XM_F16 = 0, XM_BF16 = 1, XM_F32 = 2 };
 
 // Eight signed nibbles -> eight exact f16 integers in slot order [k0,k4,k1,k5,k2,k6,k3,k7].
+// Nibbles i and i + 4 sit at bits 4i and 16 + 4i.  The even pairs (bits 0-3 / 16-19 of w and of
+// w >> 8) become 0x6400 | (v ^ 8) = 1024 + q + 8; the odd pairs are used in place, at bits 4-7 /
+// 20-23, as 0x6400 | (v ^ 8) << 4 = 1024 + 16 (q + 8) and scaled by 1/16 in the same packed FMA
+// that removes the offset.  Every intermediate is an exact f16, so q in [-8, 7] is exact, and
+// one shift serves all eight nibbles.
 __device__ __forceinline__ half8_t unpack_q4_f16(uint32_t w) {
-  const uint32_t M = 0x000F000Fu;  // nibbles i and i + 4 of the shifted word
-  const uint32_t C = 0x64086408u;  // f16 1024.0 exponent pattern | sign-flip bit of the nibble
+  const uint32_t M0 = 0x000F000Fu, C0 = 0x64086408u;  // low nibble of each half, sign-flip bit 3
+  const uint32_t M1 = 0x00F000F0u, C1 = 0x64806480u;  // high nibble of each half, sign-flip bit 7
+  const uint32_t w8 = w >> 8;
   u32x4_t d;
-  d[0] = ((w ^ C) & M) | (C & ~M);
-  d[1] = (((w >> 4) ^ C) & M) | (C & ~M);
-  d[2] = (((w >> 8) ^ C) & M) | (C & ~M);
-  d[3] = (((w >> 12) ^ C) & M) | (C & ~M);
-  half8_t h = biq::bitcast<half8_t>(d);
-  const _Float16 off = (_Float16)(-1032.0f);
-  return h + off;
+  d[0] = ((w ^ C0) & M0) | (C0 & ~M0);
+  d[1] = ((w ^ C1) & M1) | (C1 & ~M1);
+  d[2] = ((w8 ^ C0) & M0) | (C0 & ~M0);
+  d[3] = ((w8 ^ C1) & M1) | (C1 & ~M1);
+  const _Float16 o = (_Float16)1.0f, t = (_Float16)0.0625f;
+  const _Float16 a = (_Float16)(-1032.0f), b = (_Float16)(-72.0f);
+  const half8_t mul = {o, o, t, t, o, o, t, t};
+  const half8_t add = {a, a, b, b, a, a, b, b};
+  return __builtin_elementwise_fma(biq::bitcast<half8_t>(d), mul, add);
 }
 
 // 8 bf16 -> 8 f16 in slot order [0,4,1,5,2,6,3,7].
@@ -167,49 +175,69 @@ __global__ void __launch_bounds__(G::NTHREADS, 1)
 #pragma unroll
   for (int j = 0; j < WN; ++j) ncol[j] = n0 + wn * (32 * WN) + 32 * j + l32;
 
-  // ---- global -> registers for one K tile
+  // ---- global -> registers through buffer loads.  Descriptors start at the tile (scalar
+  //      registers, advanced per tile) and end at the matrix, so rows past M and packed rows past
+  //      K read as zero; columns past N get an offset beyond any range, and so do activation
+  //      groups / packed column groups past K in a partial last tile.  Offsets stay below 2^31
+  //      (host check).
+  constexpr uint32_t OOB = 0x80000000u;
+  constexpr int64_t XSZ = XMODE == XM_F32 ? 4 : 2;
+  uint32_t a_off[G::A_CHUNKS], b_off[G::B_CHUNKS];
+#pragma unroll
+  for (int it = 0; it < G::A_CHUNKS; ++it) {
+    const int c = tid + it * NT;
+    a_off[it] = (uint32_t)(((int64_t)(c / (BK / 8)) * ldx + 8 * (c % (BK / 8))) * XSZ);
+  }
+#pragma unroll
+  for (int it = 0; it < G::B_CHUNKS; ++it) {
+    const int c = tid + it * NT;
+    if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
+      const int kwr = c / (BN / 4), nc = (c % (BN / 4)) * 4;
+      b_off[it] = n0 + nc < N ? (uint32_t)(((int64_t)kwr * N + nc) * 4) : OOB;
+    } else {
+      const int nl = c / (BK / 32), part4 = c % (BK / 32);
+      b_off[it] = n0 + nl < N ? (uint32_t)(((int64_t)nl * KW + 4 * part4) * 4) : OOB;
+    }
+  }
+  auto rsrc = [](const void *base, int64_t bytes) {
+    const uint32_t n = bytes > 0x7fffffffLL ? 0x7fffffffu : (bytes < 0 ? 0u : (uint32_t)bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)n, 0x00020000);
+  };
+  // Word rows of the [N, K/8] layout are 16-byte aligned only when K % 32 == 0.
+  const bool vec_nk = (KW & 3) == 0;
+
   auto load_tile = [&](int64_t kt, TileRegs<G, XMODE> &R, float (&sc)[WN][TILE_BLOCKS]) {
+    const auto ra = rsrc(reinterpret_cast<const char *>(xv) + (m0 * ldx + kt) * XSZ,
+                         ((M - m0) * ldx - kt) * XSZ);
 #pragma unroll
     for (int it = 0; it < G::A_CHUNKS; ++it) {
-      const int c = tid + it * NT;
-      const int row = c / (BK / 8), kc = c % (BK / 8);
-      const int64_t gm = m0 + row, gk = kt + 8 * kc;
-      const bool ok = gm < M && gk < K;
+      const int kc = (tid + it * NT) % (BK / 8);
+      const uint32_t off = kt + 8 * kc < K ? a_off[it] : OOB;
       if constexpr (XMODE == XM_F32) {
-        const float4 *src =
-            reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(xv) + gm * ldx + gk);
-        R.a32[2 * it] = ok ? src[0] : make_float4(0.f, 0.f, 0.f, 0.f);
-        R.a32[2 * it + 1] = ok ? src[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+        R.a32[2 * it] = biq::bitcast<float4>(__builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
+        R.a32[2 * it + 1] = biq::bitcast<float4>(__builtin_amdgcn_raw_buffer_load_b128(ra, off + 16, 0, 0));
       } else {
-        R.a16[it] = ok ? *reinterpret_cast<const u32x4_t *>(
-                             reinterpret_cast<const uint16_t *>(xv) + gm * ldx + gk)
-                       : u32x4_t{0u, 0u, 0u, 0u};
+        R.a16[it] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
       }
     }
     const int64_t kw0 = kt / 8;
+    if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
+      const auto rb = rsrc(words + kw0 * N + n0, ((KW - kw0) * N - n0) * 4);
 #pragma unroll
-    for (int it = 0; it < G::B_CHUNKS; ++it) {
-      const int c = tid + it * NT;
-      if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
-        const int kwr = c / (BN / 4), nc = (c % (BN / 4)) * 4;
-        R.b[it] = (kw0 + kwr < KW && n0 + nc < N)
-                      ? *reinterpret_cast<const u32x4_t *>(words + (kw0 + kwr) * N + n0 + nc)
-                      : u32x4_t{0u, 0u, 0u, 0u};
-      } else {
-        const int nl = c / (BK / 32), part4 = c % (BK / 32);
-        const int64_t n = n0 + nl, kwb = kw0 + 4 * part4;
-        u32x4_t w = {0u, 0u, 0u, 0u};
-        if (n < N) {
-          const uint32_t *src = words + n * KW + kwb;
-          if ((KW & 3) == 0 && kwb + 3 < KW) {
-            w = *reinterpret_cast<const u32x4_t *>(src);
-          } else {
+      for (int it = 0; it < G::B_CHUNKS; ++it) R.b[it] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[it], 0, 0);
+    } else {
+      const auto rb = rsrc(words + n0 * KW + kw0, ((N - n0) * KW - kw0) * 4);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (kwb + j < KW) w[j] = src[j];
-          }
+      for (int it = 0; it < G::B_CHUNKS; ++it) {
+        const int part4 = (tid + it * NT) % (BK / 32);
+        const int64_t kwb = kw0 + 4 * part4;
+        if (vec_nk) {
+          R.b[it] = __builtin_amdgcn_raw_buffer_load_b128(rb, kwb < KW ? b_off[it] : OOB, 0, 0);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            R.b[it][j] = __builtin_amdgcn_raw_buffer_load_b32(rb, kwb + j < KW ? b_off[it] + 4 * j : OOB, 0, 0);
         }
-        R.b[it] = w;
       }
     }
 #pragma unroll
@@ -457,6 +485,10 @@ extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M
   if (K % 8 != 0 || K % block != 0 || N % 8 != 0)
     return biq::fail(BIQ_ERR_INVALID_ARG, "q4 linear requires K % 8 == 0, K % block == 0, N % 8 == 0");
   if (ldx < K) return biq::fail(BIQ_ERR_INVALID_ARG, "activation row stride is smaller than K");
+  // tile-relative buffer offsets are 32-bit: 256 activation rows, 16 packed rows of N words or
+  // 256 packed columns of K / 8 words must span less than 2^31 bytes
+  if (ldx >= (1LL << 21) || N >= (1LL << 24) || K >= (1LL << 24))
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "q4 linear: row stride, N or K too large for 32-bit tile offsets");
   const int esz = x_dtype == BIQ_DTYPE_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(x) & 15) || ((ldx * esz) & 15) ||
       (reinterpret_cast<uintptr_t>(words) & 15) || (reinterpret_cast<uintptr_t>(scales) & 3))

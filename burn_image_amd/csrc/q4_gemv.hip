@@ -43,15 +43,22 @@ constexpr int NK_BATCH = 2;      // super-steps of 128 k per batch -> unit of 25
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+// Exact nibble decode, slot order [k0,k4,k1,k5,k2,k6,k3,k7] (the q4_gemm.hip decode: low
+// nibbles of each half as 0x6400 | (v ^ 8), high nibbles in place scaled by 1/16 in the FMA).
 __device__ __forceinline__ half8_t unpack_q4(uint32_t w) {
-  const uint32_t M = 0x000F000Fu, C = 0x64086408u;
+  const uint32_t M0 = 0x000F000Fu, C0 = 0x64086408u;
+  const uint32_t M1 = 0x00F000F0u, C1 = 0x64806480u;
+  const uint32_t w8 = w >> 8;
   u32x4_t d;
-  d[0] = ((w ^ C) & M) | (C & ~M);
-  d[1] = (((w >> 4) ^ C) & M) | (C & ~M);
-  d[2] = (((w >> 8) ^ C) & M) | (C & ~M);
-  d[3] = (((w >> 12) ^ C) & M) | (C & ~M);
-  half8_t h = biq::bitcast<half8_t>(d);
-  return h + (_Float16)(-1032.0f);
+  d[0] = ((w ^ C0) & M0) | (C0 & ~M0);
+  d[1] = ((w ^ C1) & M1) | (C1 & ~M1);
+  d[2] = ((w8 ^ C0) & M0) | (C0 & ~M0);
+  d[3] = ((w8 ^ C1) & M1) | (C1 & ~M1);
+  const _Float16 o = (_Float16)1.0f, t = (_Float16)0.0625f;
+  const _Float16 a = (_Float16)(-1032.0f), b = (_Float16)(-72.0f);
+  const half8_t mul = {o, o, t, t, o, o, t, t};
+  const half8_t add = {a, a, b, b, a, a, b, b};
+  return __builtin_elementwise_fma(biq::bitcast<half8_t>(d), mul, add);
 }
 
 // 8 raw activations of the x dtype.
