@@ -36,6 +36,22 @@ def attn_flops(B, H, S, D):
     return 4.0 * B * H * D * S * S
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemm_attention_4608tok_hbm_traffic.json")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes (copy-kernel calibrated); None when that measurement is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if kernel == "q4_gemm":
+        return t.get("q4_gemm_traffic_bytes_per_launch")
+    return t.get("per_launch", {}).get(kernel, {}).get("traffic_bytes")
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -188,7 +204,7 @@ def main():
         "per_kernel": per_kernel,
         "roofline": {"bound": "mfma", "kernel": dom, "launches_per_step": dom_launches,
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(dom)},
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args, words_np, scales_np, x_np, q_np, k_np, v_np)

@@ -5,6 +5,8 @@
     python -m burn_image_amd.perf attention --B 1 --H 24 --Hkv 24 --S 4608 --D 128 [--dtype bf16]
                                             [--causal] [--segments 1024:64:512]
     python -m burn_image_amd.perf qk_prep --S 4608 --Hq 24 --Hkv 24 --D 128 [--dtype f32]
+    python -m burn_image_amd.perf copy --mib 512   (a plain device copy of known size: the
+                                                    calibration kernel for HBM byte counters)
     (every op also takes --iters, --warmup and --graph)
 
 Inputs are random and resident on the GPU before timing; weights rotate over enough distinct
@@ -139,6 +141,16 @@ def bench_qk_prep(a) -> dict:
             "frac_hbm_peak": round(bytes_ / us / 1e3 / PEAK_GBS, 4)}
 
 
+def bench_copy(a) -> dict:
+    dev = torch.device("cuda:0")
+    n = a.mib << 20
+    src = torch.ones(n // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    us = _time(lambda i: dst.copy_(src), a.iters, a.warmup)
+    return {"op": "copy", "bytes_read": n, "bytes_written": n, "us": round(us, 3),
+            "gbs": round(2 * n / us / 1e3, 1)}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(prog="python -m burn_image_amd.perf")
     sub = ap.add_subparsers(dest="op", required=True)
@@ -167,6 +179,8 @@ def main(argv=None):
     p.add_argument("--Hkv", type=int, default=24)
     p.add_argument("--D", type=int, default=128)
     p.add_argument("--dtype", default="f32", choices=list(DT))
+    p = sub.add_parser("copy")
+    p.add_argument("--mib", type=int, default=512)
     for p in sub.choices.values():
         p.add_argument("--iters", type=int, default=50)
         p.add_argument("--warmup", type=int, default=5)
@@ -175,7 +189,8 @@ def main(argv=None):
     global _GRAPH
     _GRAPH = a.graph
     _lib.load()
-    fn = {"q4_linear": bench_q4_linear, "attention": bench_attention, "qk_prep": bench_qk_prep}[a.op]
+    fn = {"q4_linear": bench_q4_linear, "attention": bench_attention, "qk_prep": bench_qk_prep,
+          "copy": bench_copy}[a.op]
     print(json.dumps(fn(a)), flush=True)
 
 
