@@ -3,7 +3,9 @@
 One step = one pass of the hot path at the 4608-token Boogu Turbo shape over resident synthetic
 inputs: the four packed-Q4 projection GEMMs (M 4608; K x N = 3072x9216 QKV, 3072x3072 O,
 3072x12288 MLP up, 12288x3072 MLP down; bf16 activations, f32 outputs) and the joint flash
-attention (B1 H24 S4608 D128, bf16 Q/K/V, f32 output).  Prints one JSON line.
+attention (B1 H24 S4608 D128, bf16 Q/K/V, f32 output).  Prints one JSON line.  After the timed
+steps it also times the fused SwiGLU projection (both 3072x12288 up weights in one pass) and
+reports the denoise block with it (`ms_per_denoise_block_fused_swiglu`).
 
     python bench.py [--steps 20] [--warmup 3] [--no-cpu]
 """
@@ -164,6 +166,26 @@ def main():
     per_op_ms = {name: float(np.mean([evs[s][j].elapsed_time(evs[s][j + 1]) for s in range(args.steps)]))
                  for j, (name, _) in enumerate(ops)}
 
+    # ---------------- fused SwiGLU (outside the step): silu(x W1) * (x W3) at the MLP-up shape,
+    # the reference block's two up projections in one pass (feed_forward.rs:32-36) -----------
+    _, Ku, Nu = GEMMS[2]
+    w3n, s3n = W.q4_weight(3, 9, Ku, Nu, layout=1)
+    w3 = B.from_packed(torch.from_numpy(w3n.view(np.int32)).to(dev), torch.from_numpy(s3n).to(dev),
+                       1, 128, (Ku, Nu))
+    gated = torch.empty((M_TOKENS, Nu), dtype=torch.bfloat16, device=dev)
+    glu = lambda: B.q_matmul_swiglu(xs["mlp_up"], weights["mlp_up"], w3, out=gated)  # noqa: E731
+    for _ in range(args.warmup):
+        glu()
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    g0.record(stream)
+    for _ in range(args.steps):
+        glu()
+    g1.record(stream)
+    torch.cuda.synchronize()
+    glu_ms = g0.elapsed_time(g1) / args.steps
+    glu_fl = 2 * gemm_flops(M_TOKENS, Ku, Nu)
+
     gemm_ms = sum(per_op_ms[n] for n, _, _ in GEMMS)
     gemm_fl = sum(flops[n] for n, _, _ in GEMMS)
     attn_ms = per_op_ms["attention"]
@@ -201,7 +223,12 @@ def main():
         "frac_peak": round(step_flops / (ms_per_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "ms_per_denoise_block": round(block_ms, 4),
         "ms_per_denoise_block_1xup": round(block_ms - per_op_ms["mlp_up"], 4),
+        "ms_per_denoise_block_fused_swiglu": round(
+            per_op_ms["qkv"] + attn_ms + per_op_ms["o"] + glu_ms + per_op_ms["mlp_down"], 4),
         "per_kernel": per_kernel,
+        "fused_swiglu": {"ms": round(glu_ms, 4), "tflops": round(glu_fl / (glu_ms * 1e-3) / 1e12, 2),
+                         "frac_peak": round(glu_fl / (glu_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                         "shape": f"M{M_TOKENS} K{Ku} N{Nu} x2 weights, bf16 in, bf16 gated out"},
         "roofline": {"bound": "mfma", "kernel": dom, "launches_per_step": dom_launches,
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(dom)},

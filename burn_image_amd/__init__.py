@@ -6,7 +6,8 @@ from ._lib import BiqError, InvalidArgument, Unsupported, version
 from .attention import (F16_STORAGE_F32_ACCUM, STRICT_F32, AttentionKernel,
                         NativeQ4FlashAttention, RmsNorm, attention,
                         effective_portable_query_chunk_size, qk_norm_rope)
-from .linear import Linear, linear_forward, q_matmul, qwen_linear_forward
+from .linear import (Linear, LuminaFeedForward, linear_forward, q_matmul, q_matmul_swiglu,
+                     qwen_linear_forward)
 from .q4 import (BOOGU_DENOISER, FLUX_VAE, QWEN3_VL, Q4Weight, from_packed,
                  q4s_storage_block_and_axis, q4s_stored_dtype, quantize_q4s_block128_f32,
                  quantize_row_layout_q4s_block_up_to128_f32)
@@ -17,7 +18,8 @@ Q4_NK_AXIS0 = _lib.Q4_NK_AXIS0
 __all__ = [
     "AttentionKernel", "NativeQ4FlashAttention", "attention", "effective_portable_query_chunk_size",
     "RmsNorm", "qk_norm_rope", "STRICT_F32", "F16_STORAGE_F32_ACCUM",
-    "Linear", "linear_forward", "q_matmul", "qwen_linear_forward", "Q4Weight", "from_packed",
+    "Linear", "LuminaFeedForward", "linear_forward", "q_matmul", "q_matmul_swiglu",
+    "qwen_linear_forward", "Q4Weight", "from_packed",
     "q4s_storage_block_and_axis", "q4s_stored_dtype", "quantize_q4s_block128_f32",
     "quantize_row_layout_q4s_block_up_to128_f32", "BiqError", "InvalidArgument", "Unsupported",
     "version", "BOOGU_DENOISER", "QWEN3_VL", "FLUX_VAE", "Q4_KN_AXIS1", "Q4_NK_AXIS0",

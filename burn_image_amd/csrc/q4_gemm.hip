@@ -123,8 +123,11 @@ struct Geo {
 #ifndef BIQ_GEMM_WAVES
 #define BIQ_GEMM_WAVES 2, 2, 2, 4
 #endif
+#ifndef BIQ_GEMM_BK
+#define BIQ_GEMM_BK 128
+#endif
 template <int XMODE, int BLK>
-using GemmGeo = Geo<BIQ_GEMM_WAVES, (XMODE == XM_F32 || BLK <= 16) ? 64 : 128>;
+using GemmGeo = Geo<BIQ_GEMM_WAVES, (XMODE == XM_F32 || BLK <= 16) ? 64 : BIQ_GEMM_BK>;
 
 // Per-thread register copy of one tile's global data.
 template <class G, int XMODE>
@@ -134,13 +137,21 @@ struct TileRegs {
   u32x4_t b[G::B_CHUNKS];
 };
 
-template <class G, int LAYOUT, int XMODE, int BLK>
-__global__ void __launch_bounds__(G::NTHREADS, 1)
+// GLU: the SwiGLU form y = silu(x . W1) * (x . W3) of the reference's feed-forward
+// (crates/burn_boogu/src/model/feed_forward.rs:32-36).  A workgroup then covers BN / 2 output
+// columns of both weights: the word tile holds W1's columns in its first half and W3's in its
+// second, so a wave's two 32-column MFMA tiles are W1 and W3 for the SAME output columns and the
+// epilogue combines them in registers.
+template <class G, int LAYOUT, int XMODE, int BLK, bool GLU>
+__global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     q4_gemm_kernel(const void *__restrict__ xv, int64_t ldx, const uint32_t *__restrict__ words,
-                   const float *__restrict__ scales, const float *__restrict__ bias,
+                   const float *__restrict__ scales, const uint32_t *__restrict__ words3,
+                   const float *__restrict__ scales3, const float *__restrict__ bias,
                    void *__restrict__ yv, int y_dtype, int64_t M, int64_t N, int64_t K,
                    int tiles_m, int tiles_n) {
   constexpr int WM = G::WM, WN = G::WN, BM = G::BM, BN = G::BN, NT = G::NTHREADS;
+  static_assert(!GLU || WN == 2, "the SwiGLU form pairs the two column tiles of a wave");
+  constexpr int BNO = GLU ? BN / 2 : BN;  // output columns per workgroup
   constexpr int BK = G::BK, A_LD = G::A_LD;
   constexpr int B_LD = BN;  // LDS row stride of the word tile, in words
   constexpr int NSPLIT = XMODE == XM_F32 ? 2 : 1;
@@ -167,13 +178,14 @@ __global__ void __launch_bounds__(G::NTHREADS, 1)
   const int64_t gsize = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
   const int64_t tile_m = first_m + (pid % in_group) % gsize;
   const int64_t tile_n = (pid % in_group) / gsize;
-  const int64_t m0 = tile_m * BM, n0 = tile_n * BN;
+  const int64_t m0 = tile_m * BM, n0 = tile_n * BNO;
   const int64_t nblk = K / BLK;
   const int64_t KW = K / 8;
 
   int64_t ncol[WN];
 #pragma unroll
-  for (int j = 0; j < WN; ++j) ncol[j] = n0 + wn * (32 * WN) + 32 * j + l32;
+  for (int j = 0; j < WN; ++j)
+    ncol[j] = GLU ? n0 + wn * 32 + l32 : n0 + wn * (32 * WN) + 32 * j + l32;
 
   // ---- global -> registers through buffer loads.  Descriptors start at the tile (scalar
   //      registers, advanced per tile) and end at the matrix, so rows past M and packed rows past
@@ -183,6 +195,7 @@ __global__ void __launch_bounds__(G::NTHREADS, 1)
   constexpr uint32_t OOB = 0x80000000u;
   constexpr int64_t XSZ = XMODE == XM_F32 ? 4 : 2;
   uint32_t a_off[G::A_CHUNKS], b_off[G::B_CHUNKS];
+  bool b_w3[G::B_CHUNKS];  // GLU: this word group comes from W3
 #pragma unroll
   for (int it = 0; it < G::A_CHUNKS; ++it) {
     const int c = tid + it * NT;
@@ -192,10 +205,16 @@ __global__ void __launch_bounds__(G::NTHREADS, 1)
   for (int it = 0; it < G::B_CHUNKS; ++it) {
     const int c = tid + it * NT;
     if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
-      const int kwr = c / (BN / 4), nc = (c % (BN / 4)) * 4;
+      const int kwr = c / (BN / 4);
+      int nc = (c % (BN / 4)) * 4;
+      b_w3[it] = GLU && nc >= BNO;
+      nc -= b_w3[it] ? BNO : 0;
       b_off[it] = n0 + nc < N ? (uint32_t)(((int64_t)kwr * N + nc) * 4) : OOB;
     } else {
-      const int nl = c / (BK / 32), part4 = c % (BK / 32);
+      const int part4 = c % (BK / 32);
+      int nl = c / (BK / 32);
+      b_w3[it] = GLU && nl >= BNO;
+      nl -= b_w3[it] ? BNO : 0;
       b_off[it] = n0 + nl < N ? (uint32_t)(((int64_t)nl * KW + 4 * part4) * 4) : OOB;
     }
   }
@@ -221,22 +240,37 @@ __global__ void __launch_bounds__(G::NTHREADS, 1)
       }
     }
     const int64_t kw0 = kt / 8;
+    // GLU: both weights are read with the same offsets; the lanes of the other weight pass an
+    // out-of-range offset (zero, no memory access) and the two results are OR-ed.
+    auto ld128 = [&](const __amdgpu_buffer_rsrc_t &r1, const __amdgpu_buffer_rsrc_t &r3, uint32_t off,
+                     bool w3) -> u32x4_t {
+      if constexpr (!GLU) return __builtin_amdgcn_raw_buffer_load_b128(r1, off, 0, 0);
+      return __builtin_amdgcn_raw_buffer_load_b128(r1, w3 ? OOB : off, 0, 0) |
+             __builtin_amdgcn_raw_buffer_load_b128(r3, w3 ? off : OOB, 0, 0);
+    };
+    auto ld32 = [&](const __amdgpu_buffer_rsrc_t &r1, const __amdgpu_buffer_rsrc_t &r3, uint32_t off,
+                    bool w3) -> uint32_t {
+      if constexpr (!GLU) return __builtin_amdgcn_raw_buffer_load_b32(r1, off, 0, 0);
+      return __builtin_amdgcn_raw_buffer_load_b32(r1, w3 ? OOB : off, 0, 0) |
+             __builtin_amdgcn_raw_buffer_load_b32(r3, w3 ? off : OOB, 0, 0);
+    };
     if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
       const auto rb = rsrc(words + kw0 * N + n0, ((KW - kw0) * N - n0) * 4);
+      const auto rb3 = rsrc((GLU ? words3 : words) + kw0 * N + n0, ((KW - kw0) * N - n0) * 4);
 #pragma unroll
-      for (int it = 0; it < G::B_CHUNKS; ++it) R.b[it] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[it], 0, 0);
+      for (int it = 0; it < G::B_CHUNKS; ++it) R.b[it] = ld128(rb, rb3, b_off[it], b_w3[it]);
     } else {
       const auto rb = rsrc(words + n0 * KW + kw0, ((N - n0) * KW - kw0) * 4);
+      const auto rb3 = rsrc((GLU ? words3 : words) + n0 * KW + kw0, ((N - n0) * KW - kw0) * 4);
 #pragma unroll
       for (int it = 0; it < G::B_CHUNKS; ++it) {
         const int part4 = (tid + it * NT) % (BK / 32);
         const int64_t kwb = kw0 + 4 * part4;
         if (vec_nk) {
-          R.b[it] = __builtin_amdgcn_raw_buffer_load_b128(rb, kwb < KW ? b_off[it] : OOB, 0, 0);
+          R.b[it] = ld128(rb, rb3, kwb < KW ? b_off[it] : OOB, b_w3[it]);
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            R.b[it][j] = __builtin_amdgcn_raw_buffer_load_b32(rb, kwb + j < KW ? b_off[it] + 4 * j : OOB, 0, 0);
+          for (int j = 0; j < 4; ++j) R.b[it][j] = ld32(rb, rb3, kwb + j < KW ? b_off[it] + 4 * j : OOB, b_w3[it]);
         }
       }
     }
@@ -244,7 +278,7 @@ __global__ void __launch_bounds__(G::NTHREADS, 1)
     for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int t = 0; t < TILE_BLOCKS; ++t)
-        sc[j][t] = load_scale<LAYOUT>(scales, kt / BLK + t, ncol[j], N, nblk);
+        sc[j][t] = load_scale<LAYOUT>(GLU && j == 1 ? scales3 : scales, kt / BLK + t, ncol[j], N, nblk);
   };
 
   // ---- registers -> LDS buffer (activation conversion to f16 slot order happens here)
@@ -289,7 +323,8 @@ __global__ void __launch_bounds__(G::NTHREADS, 1)
         a[i][x] = *reinterpret_cast<const half8_t *>(
             &As[buf][x][(wm * (32 * WM) + 32 * i + l32) * A_LD + 16 * s + 8 * lh]);
 #pragma unroll
-    for (int j = 0; j < WN; ++j) w[j] = Bs[buf][(2 * s + lh) * B_LD + wn * (32 * WN) + 32 * j + l32];
+    for (int j = 0; j < WN; ++j)
+      w[j] = Bs[buf][(2 * s + lh) * B_LD + (GLU ? j * BNO + wn * 32 : wn * (32 * WN) + 32 * j) + l32];
   };
 
   // Pipeline: R holds tile t+1 while tile t computes; tile t+1 is stored into the other LDS
@@ -391,19 +426,23 @@ __global__ void __launch_bounds__(G::NTHREADS, 1)
     }
   }
 
-  // ---------------- epilogue: bias, convert, store ------------------------------------------
+  // ---------------- epilogue: bias (or the SwiGLU gate), convert, store ---------------------
 #pragma unroll
-  for (int j = 0; j < WN; ++j) {
+  for (int j = 0; j < (GLU ? 1 : WN); ++j) {
     const int64_t col = ncol[j];
     if (col >= N) continue;
-    const float bv = bias ? bias[col] : 0.0f;
+    const float bv = (!GLU && bias) ? bias[col] : 0.0f;
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + wm * (32 * WM) + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (row >= M) continue;
-        const float v = acc[i][j][r] + bv;
+        float v = acc[i][j][r] + bv;
+        if constexpr (GLU) {
+          // silu(a) = a / (1 + e^-a), times the W3 projection of the same row and column
+          v = v / (1.0f + __expf(-v)) * acc[i][1][r];
+        }
         if (y_dtype == BIQ_DTYPE_F32) {
           reinterpret_cast<float *>(yv)[row * N + col] = v;
         } else if (y_dtype == BIQ_DTYPE_F16) {
@@ -415,47 +454,48 @@ __global__ void __launch_bounds__(G::NTHREADS, 1)
   }
 }
 
-template <int LAYOUT, int XMODE>
-int launch_blk(hipStream_t s, int block, const void *x, int64_t ldx, const uint32_t *words,
-               const float *scales, const float *bias, void *y, int y_dtype, int64_t M, int64_t N,
-               int64_t K) {
+// Weights of one launch: W (and W3 for the SwiGLU form).
+struct Q4Args {
+  const uint32_t *words, *words3;
+  const float *scales, *scales3;
+};
+
+template <int LAYOUT, int XMODE, bool GLU>
+int launch_blk(hipStream_t s, int block, const void *x, int64_t ldx, const Q4Args &w,
+               const float *bias, void *y, int y_dtype, int64_t M, int64_t N, int64_t K) {
   using G8 = GemmGeo<XMODE, 8>;
   using G16 = GemmGeo<XMODE, 16>;
   using G = GemmGeo<XMODE, 128>;
-  const int tiles_m = (int)((M + G::BM - 1) / G::BM), tiles_n = (int)((N + G::BN - 1) / G::BN);
+  constexpr int BNO = GLU ? G::BN / 2 : G::BN;
+  const int tiles_m = (int)((M + G::BM - 1) / G::BM), tiles_n = (int)((N + BNO - 1) / BNO);
   dim3 grid((unsigned)((int64_t)tiles_m * tiles_n));
   dim3 blk(G::NTHREADS);
-#define BIQ_LAUNCH(B)                                                                              \
-  hipLaunchKernelGGL((q4_gemm_kernel<G, LAYOUT, XMODE, B>), grid, blk, 0, s, x, ldx, words,       \
-                     scales, bias, y, y_dtype, M, N, K, tiles_m, tiles_n)
+#define BIQ_LAUNCH(GG, B)                                                                          \
+  hipLaunchKernelGGL((q4_gemm_kernel<GG, LAYOUT, XMODE, B, GLU>), grid, blk, 0, s, x, ldx,        \
+                     w.words, w.scales, w.words3, w.scales3, bias, y, y_dtype, M, N, K, tiles_m,  \
+                     tiles_n)
   switch (block) {
-    case 8:
-      hipLaunchKernelGGL((q4_gemm_kernel<G8, LAYOUT, XMODE, 8>), grid, blk, 0, s, x, ldx, words,
-                         scales, bias, y, y_dtype, M, N, K, tiles_m, tiles_n);
-      break;
-    case 16:
-      hipLaunchKernelGGL((q4_gemm_kernel<G16, LAYOUT, XMODE, 16>), grid, blk, 0, s, x, ldx, words,
-                         scales, bias, y, y_dtype, M, N, K, tiles_m, tiles_n);
-      break;
-    case 32: BIQ_LAUNCH(32); break;
-    case 64: BIQ_LAUNCH(64); break;
-    default: BIQ_LAUNCH(128); break;
+    case 8: BIQ_LAUNCH(G8, 8); break;
+    case 16: BIQ_LAUNCH(G16, 16); break;
+    case 32: BIQ_LAUNCH(G, 32); break;
+    case 64: BIQ_LAUNCH(G, 64); break;
+    default: BIQ_LAUNCH(G, 128); break;
   }
 #undef BIQ_LAUNCH
-  return biq::check_launch("q4 linear");
+  return biq::check_launch(GLU ? "q4 linear swiglu" : "q4 linear");
 }
 
-template <int LAYOUT>
+template <int LAYOUT, bool GLU>
 int launch_layout(hipStream_t s, int x_dtype, int block, const void *x, int64_t ldx,
-                  const uint32_t *words, const float *scales, const float *bias, void *y,
-                  int y_dtype, int64_t M, int64_t N, int64_t K) {
+                  const Q4Args &w, const float *bias, void *y, int y_dtype, int64_t M, int64_t N,
+                  int64_t K) {
   switch (x_dtype) {
     case BIQ_DTYPE_BF16:
-      return launch_blk<LAYOUT, XM_BF16>(s, block, x, ldx, words, scales, bias, y, y_dtype, M, N, K);
+      return launch_blk<LAYOUT, XM_BF16, GLU>(s, block, x, ldx, w, bias, y, y_dtype, M, N, K);
     case BIQ_DTYPE_F16:
-      return launch_blk<LAYOUT, XM_F16>(s, block, x, ldx, words, scales, bias, y, y_dtype, M, N, K);
+      return launch_blk<LAYOUT, XM_F16, GLU>(s, block, x, ldx, w, bias, y, y_dtype, M, N, K);
     default:
-      return launch_blk<LAYOUT, XM_F32>(s, block, x, ldx, words, scales, bias, y, y_dtype, M, N, K);
+      return launch_blk<LAYOUT, XM_F32, GLU>(s, block, x, ldx, w, bias, y, y_dtype, M, N, K);
   }
 }
 
@@ -467,10 +507,11 @@ int q4_gemv_launch(hipStream_t s, const void *x, int x_dtype, int64_t M, int64_t
                    const float *bias, float *y);
 }
 
-extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K,
-                             int64_t ldx, const uint32_t *words, const float *scales, int layout,
-                             int block, int64_t N, const float *bias, void *y, int y_dtype) {
-  biq::clear_error();
+namespace {
+
+// Argument checks shared by the plain and the SwiGLU entry points (BIQ_* status).
+int check_linear(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint32_t *words,
+                 const float *scales, int layout, int block, int64_t N, const void *y, int y_dtype) {
   if (!x || !words || !scales || !y) return biq::fail(BIQ_ERR_INVALID_ARG, "null pointer argument");
   if (layout != BIQ_Q4_KN_AXIS1 && layout != BIQ_Q4_NK_AXIS0)
     return biq::fail(BIQ_ERR_INVALID_ARG, "unknown Q4 layout");
@@ -494,19 +535,45 @@ extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M
       (reinterpret_cast<uintptr_t>(words) & 15) || (reinterpret_cast<uintptr_t>(scales) & 3))
     return biq::fail(BIQ_ERR_INVALID_ARG,
                      "q4 linear requires 16-byte aligned activation rows and packed words");
-  using G0 = GemmGeo<BIQ_DTYPE_BF16, 128>;
-  const int64_t tiles = ((M + G0::BM - 1) / G0::BM) * ((N + G0::BN - 1) / G0::BN);
+  using G0 = GemmGeo<XM_BF16, 128>;
+  const int64_t tiles = ((M + G0::BM - 1) / G0::BM) * ((2 * N + G0::BN - 1) / G0::BN);
   if (tiles > 0x7fffffffLL)
     return biq::fail(BIQ_ERR_UNSUPPORTED, "q4 linear output has too many tiles for one launch");
+  return BIQ_OK;
+}
+
+}  // namespace
+
+extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K,
+                             int64_t ldx, const uint32_t *words, const float *scales, int layout,
+                             int block, int64_t N, const float *bias, void *y, int y_dtype) {
+  biq::clear_error();
+  const int st = check_linear(x, x_dtype, M, K, ldx, words, scales, layout, block, N, y, y_dtype);
+  if (st != BIQ_OK) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // Up to 16 rows with an f32 output stream the weights through the small-M kernel
   // (q4_gemv.hip): split-K over the whole chip instead of N / 256 workgroups of 128 rows.
   if (M <= 16 && y_dtype == BIQ_DTYPE_F32)
     return biq::q4_gemv_launch(s, x, x_dtype, M, K, ldx, words, scales, layout, block, N, bias,
                                reinterpret_cast<float *>(y));
+  const Q4Args w{words, nullptr, scales, nullptr};
   if (layout == BIQ_Q4_KN_AXIS1)
-    return launch_layout<BIQ_Q4_KN_AXIS1>(s, x_dtype, block, x, ldx, words, scales, bias, y, y_dtype,
-                                          M, N, K);
-  return launch_layout<BIQ_Q4_NK_AXIS0>(s, x_dtype, block, x, ldx, words, scales, bias, y, y_dtype,
-                                        M, N, K);
+    return launch_layout<BIQ_Q4_KN_AXIS1, false>(s, x_dtype, block, x, ldx, w, bias, y, y_dtype, M, N, K);
+  return launch_layout<BIQ_Q4_NK_AXIS0, false>(s, x_dtype, block, x, ldx, w, bias, y, y_dtype, M, N, K);
+}
+
+extern "C" int biq_q4_linear_swiglu(void *stream, const void *x, int x_dtype, int64_t M, int64_t K,
+                                    int64_t ldx, const uint32_t *words1, const float *scales1,
+                                    const uint32_t *words3, const float *scales3, int layout,
+                                    int block, int64_t N, void *y, int y_dtype) {
+  biq::clear_error();
+  int st = check_linear(x, x_dtype, M, K, ldx, words1, scales1, layout, block, N, y, y_dtype);
+  if (st != BIQ_OK) return st;
+  st = check_linear(x, x_dtype, M, K, ldx, words3, scales3, layout, block, N, y, y_dtype);
+  if (st != BIQ_OK) return st;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const Q4Args w{words1, words3, scales1, scales3};
+  if (layout == BIQ_Q4_KN_AXIS1)
+    return launch_layout<BIQ_Q4_KN_AXIS1, true>(s, x_dtype, block, x, ldx, w, nullptr, y, y_dtype, M, N, K);
+  return launch_layout<BIQ_Q4_NK_AXIS0, true>(s, x_dtype, block, x, ldx, w, nullptr, y, y_dtype, M, N, K);
 }

@@ -91,3 +91,61 @@ def qwen_linear_forward(linear: Linear, input: torch.Tensor, **kw) -> torch.Tens
     if linear.weight.layout != _lib.Q4_NK_AXIS0:
         raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "Qwen linear weights use the [N, K] layout")
     return q_matmul(input, linear.weight, bias=linear.bias, **kw)
+
+
+def q_matmul_swiglu(lhs: torch.Tensor, w1: Q4Weight, w3: Q4Weight, out: Optional[torch.Tensor] = None,
+                    out_dtype: Optional[torch.dtype] = None, stream: Optional[int] = None) -> torch.Tensor:
+    """silu(lhs . W1) * (lhs . W3) in one pass over lhs: the gated half of the SwiGLU
+    feed-forward (crates/burn_boogu/src/model/feed_forward.rs:32-36).  Both weights must share
+    layout, block and shape; the output dtype defaults to float32 (the reference's lhs dtype)."""
+    for w in (w1, w3):
+        if not isinstance(w, Q4Weight):
+            raise _lib.Unsupported(_lib.ERR_UNSUPPORTED, "q_matmul_swiglu accelerates packed-Q4 weights only")
+        if w.block not in SUPPORTED_BLOCKS:
+            raise _lib.Unsupported(_lib.ERR_UNSUPPORTED, f"Q4 block {w.block} is not supported")
+    if (w1.layout, w1.block, w1.shape) != (w3.layout, w3.block, w3.shape):
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "the two gated projections must share layout, block and shape")
+    if lhs.dtype not in _DTYPE_CODE:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, f"lhs dtype {lhs.dtype} is not supported")
+    if not lhs.is_cuda:
+        raise ValueError("lhs must be a GPU tensor")
+    K, N = w1.K, w1.N
+    if lhs.shape[-1] != K:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG,
+                                   f"lhs width {lhs.shape[-1]} does not match weight input {K}")
+    lead = lhs.shape[:-1]
+    x = lhs.reshape(-1, K)
+    if x.stride(-1) != 1 or (x.shape[0] > 1 and x.stride(0) < K):
+        x = x.contiguous()
+    M = x.shape[0]
+    ldx = x.stride(0) if M > 1 else K
+    odt = out_dtype or (out.dtype if out is not None else torch.float32)
+    if out is None:
+        out = torch.empty((M, N), dtype=odt, device=lhs.device)
+    elif out.dtype != odt or out.numel() != M * N or not out.is_contiguous():
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "out must be a contiguous [M, N] tensor")
+    s = torch.cuda.current_stream(lhs.device).cuda_stream if stream is None else stream
+    _lib.check(_lib.load().biq_q4_linear_swiglu(
+        s, x.data_ptr(), _DTYPE_CODE[x.dtype], M, K, ldx, w1.words.data_ptr(), w1.scales.data_ptr(),
+        w3.words.data_ptr(), w3.scales.data_ptr(), w1.layout, w1.block, N, out.data_ptr(),
+        _DTYPE_CODE[odt]))
+    return out.reshape(*lead, N)
+
+
+@dataclass
+class LuminaFeedForward:
+    """SwiGLU feed-forward (crates/burn_boogu/src/model/feed_forward.rs:5-37): bias-free
+    linear_1 / linear_3 (width -> inner) and linear_2 (inner -> width), all packed Q4 [K, N]."""
+    linear_1: Linear
+    linear_2: Linear
+    linear_3: Linear
+
+    def forward(self, x: torch.Tensor, hidden_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """linear_2(silu(linear_1(x)) * linear_3(x)); the gated hidden state is produced by one
+        fused pass (f32 by default, as the reference; `hidden_dtype` may narrow it)."""
+        for lin in (self.linear_1, self.linear_3):
+            if lin.weight.layout != _lib.Q4_KN_AXIS1 or lin.bias is not None:
+                raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG,
+                                           "the feed-forward's gated projections are bias-free [K, N] weights")
+        gated = q_matmul_swiglu(x, self.linear_1.weight, self.linear_3.weight, out_dtype=hidden_dtype)
+        return linear_forward(self.linear_2, gated)

@@ -1,7 +1,7 @@
 """Per-operator microbenchmarks of libbiq on one GPU (HIP-event timing, JSON output).
 
     python -m burn_image_amd.perf q4_linear --M 4608 --K 3072 --N 9216 [--layout 1] [--block 128]
-                                            [--xdtype bf16] [--ydtype f32] [--iters 50]
+                                            [--xdtype bf16] [--ydtype f32] [--iters 50] [--swiglu]
     python -m burn_image_amd.perf attention --B 1 --H 24 --Hkv 24 --S 4608 --D 128 [--dtype bf16]
                                             [--causal] [--segments 1024:64:512]
     python -m burn_image_amd.perf qk_prep --S 4608 --Hq 24 --Hkv 24 --D 128 [--dtype f32]
@@ -23,7 +23,7 @@ import torch
 
 from . import _lib
 from .attention import RmsNorm, attention, qk_norm_rope
-from .linear import q_matmul
+from .linear import q_matmul, q_matmul_swiglu
 from .q4 import from_packed
 
 DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
@@ -80,11 +80,21 @@ def bench_q4_linear(a) -> dict:
         weights.append(from_packed(words, scales, a.layout, a.block, (K, N) if a.layout == 1 else (N, K)))
     x = torch.randn((M, K), device=dev, generator=g).to(DT[a.xdtype])
     y = torch.empty((M, N), dtype=DT[a.ydtype], device=dev)
-    us = _time(lambda i: q_matmul(x, weights[i % copies], out=y), a.iters, a.warmup)
-    flops = 2.0 * M * N * K
+    if a.swiglu:  # silu(x W1) * (x W3): consecutive weight copies serve as W1 and W3
+        if copies == 1:
+            weights.append(from_packed(weights[0].words.clone(), weights[0].scales.clone(), a.layout,
+                                       a.block, weights[0].shape))
+        nw = len(weights)
+        us = _time(lambda i: q_matmul_swiglu(x, weights[i % nw], weights[(i + 1) % nw], out=y),
+                   a.iters, a.warmup)
+        flops, wbytes = 4.0 * M * N * K, 2 * wbytes
+    else:
+        us = _time(lambda i: q_matmul(x, weights[i % copies], out=y), a.iters, a.warmup)
+        flops = 2.0 * M * N * K
     ebytes = {"f32": 4, "f16": 2, "bf16": 2}
     bytes_ = wbytes + M * K * ebytes[a.xdtype] + M * N * ebytes[a.ydtype]
-    return {"op": "q4_linear", "M": M, "K": K, "N": N, "layout": a.layout, "block": a.block,
+    return {"op": "q4_linear_swiglu" if a.swiglu else "q4_linear", "M": M, "K": K, "N": N,
+            "layout": a.layout, "block": a.block,
             "xdtype": a.xdtype, "ydtype": a.ydtype, "weight_copies": copies, "us": round(us, 3),
             "tflops": round(flops / us / 1e6, 2), "frac_mfma_peak": round(flops / us / 1e6 / PEAK_TFLOPS, 4),
             "gbs": round(bytes_ / us / 1e3, 1), "frac_hbm_peak": round(bytes_ / us / 1e3 / PEAK_GBS, 4)}
@@ -163,6 +173,7 @@ def main(argv=None):
     p.add_argument("--xdtype", default="bf16", choices=list(DT))
     p.add_argument("--ydtype", default="f32", choices=list(DT))
     p.add_argument("--rotate-bytes", type=float, default=0.0)
+    p.add_argument("--swiglu", action="store_true", help="fused silu(x W1) * (x W3) over two weights")
     p = sub.add_parser("attention")
     p.add_argument("--B", type=int, default=1)
     p.add_argument("--H", type=int, default=24)

@@ -93,6 +93,16 @@ int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K
                   const uint32_t *words, const float *scales, int layout, int block, int64_t N,
                   const float *bias, void *y, int y_dtype);
 
+/* y[M, N] = silu(x . W1) * (x . W3), the gated half of the SwiGLU feed-forward
+ * `silu(linear_1(x)) * linear_3(x)` (crates/burn_boogu/src/model/feed_forward.rs:32-36), whose
+ * output feeds linear_2.  One pass over x computes both projections (same layout, block, K and N;
+ * bias-free, as the reference's FFN) and the gate in f32 before the y_dtype store; silu(a) =
+ * a / (1 + e^-a).  Arguments and requirements as biq_q4_linear, per weight. */
+int biq_q4_linear_swiglu(void *stream, const void *x, int x_dtype, int64_t M, int64_t K,
+                         int64_t ldx, const uint32_t *words1, const float *scales1,
+                         const uint32_t *words3, const float *scales3, int layout, int block,
+                         int64_t N, void *y, int y_dtype);
+
 /* Exact attention O = softmax(Q K^T * scale + mask) V, the operator behind
  * AttentionKernel::execute / execute_gqa (crates/burn_boogu/src/model/attention.rs:47-105), the
  * padded-blackbox flash kernel (native_flash.rs:1006-1090) and Burn's attention op

@@ -257,3 +257,66 @@ def test_gpu_q4_linear_small_m_deterministic_and_graph_replay(gpu, oracle):
         torch.cuda.synchronize()
         assert torch.equal(out, y0), f"replay {i}"
         B.q_matmul(xd[:1], q)  # unrelated eager work between replays
+
+
+def silu_gate_ref(y1, y3):
+    """silu(a) * b in float64 (feed_forward.rs:32-36)."""
+    y1 = y1.astype(np.float64)
+    return (y1 / (1.0 + np.exp(-y1)) * y3.astype(np.float64)).astype(np.float32)
+
+
+@pytest.mark.parametrize("layout", [1, 0])
+@pytest.mark.parametrize("block", [8, 32, 128])
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+def test_gpu_q4_swiglu_blocks_dtypes_tails(gpu, oracle, layout, block, xdt):
+    """Fused silu(x.W1) * (x.W3): column tail (N = 200, not a multiple of the 128-column tile),
+    row tail (M = 77), both layouts, small and large blocks, 16- and 32-bit activations."""
+    M, K, N = 77, (648 if block == 8 else 640), 200
+    x = W.activations(19, block + layout, M, K, xdt)
+    w1, s1 = W.q4_weight(19, 1 + block + layout, K, N, layout=layout, block=block)
+    w3, s3 = W.q4_weight(19, 2 + block + layout, K, N, layout=layout, block=block)
+    q1, q3 = weight(w1, s1, layout, block, K, N, gpu), weight(w3, s3, layout, block, K, N, gpu)
+    y = host(B.q_matmul_swiglu(dev(x, TORCH_DT[xdt], gpu), q1, q3))
+    ref = silu_gate_ref(oracle.q4_linear_f64(x, w1, s1, layout, block, N),
+                        oracle.q4_linear_f64(x, w3, s3, layout, block, N))
+    assert_parity(y, ref, f"swiglu_blk{block}_l{layout}_{xdt}")
+
+
+def test_gpu_q4_swiglu_feed_forward_and_dtypes(gpu, oracle):
+    """LuminaFeedForward: linear_2(silu(linear_1 x) * linear_3 x) against the oracle's three
+    f64 GEMMs with the f32-rounded gated state in between; bf16 / f16 gated outputs within their
+    rounding of the f32 gate."""
+    M, width, inner = 130, 256, 384
+    x = W.activations(20, 1, M, width, "bf16")
+    w1, s1 = W.q4_weight(20, 2, width, inner, layout=1)
+    w3, s3 = W.q4_weight(20, 3, width, inner, layout=1)
+    w2, s2 = W.q4_weight(20, 4, inner, width, layout=1)
+    lin = [B.Linear(weight(w, s, 1, 128, k, n, gpu)) for (w, s, k, n) in
+           ((w1, s1, width, inner), (w2, s2, inner, width), (w3, s3, width, inner))]
+    ffn = B.LuminaFeedForward(*lin)
+    xd = dev(x, torch.bfloat16, gpu)
+    gated = silu_gate_ref(oracle.q4_linear_f64(x, w1, s1, 1, 128, inner),
+                          oracle.q4_linear_f64(x, w3, s3, 1, 128, inner))
+    ref = oracle.q4_linear_f64(gated, w2, s2, 1, 128, width).astype(np.float32)
+    assert_parity(host(ffn.forward(xd)), ref, "lumina_ffn")
+    g16 = host(B.q_matmul_swiglu(xd, lin[0].weight, lin[2].weight, out_dtype=torch.float16))
+    assert np.max(np.abs(g16 - gated)) <= np.max(np.abs(gated)) * 2.0 ** -10
+    gb = host(B.q_matmul_swiglu(xd, lin[0].weight, lin[2].weight, out_dtype=torch.bfloat16))
+    assert np.max(np.abs(gb - gated)) <= np.max(np.abs(gated)) * 2.0 ** -7
+    with pytest.raises(B.InvalidArgument, match="share layout"):
+        B.q_matmul_swiglu(xd, lin[0].weight, lin[1].weight)
+
+
+def test_gpu_q4_swiglu_released_width(gpu, oracle):
+    """Released Boogu FFN width: 3360 -> 13568 with block-32 scales, sampled rows."""
+    K, N, M = 3360, 13568, 256
+    blk = oracle.q4_kn_block(K, N)
+    x = W.activations(21, 1, M, K, "f32")
+    w1, s1 = W.q4_weight(21, 2, K, N, layout=1, block=blk)
+    w3, s3 = W.q4_weight(21, 3, K, N, layout=1, block=blk)
+    y = host(B.q_matmul_swiglu(dev(x, device=gpu), weight(w1, s1, 1, blk, K, N, gpu),
+                               weight(w3, s3, 1, blk, K, N, gpu)))
+    rows = sample_rows(M, n=24, seed=21)
+    ref = silu_gate_ref(oracle.q4_linear_f64(x, w1, s1, 1, blk, N, rows=rows),
+                        oracle.q4_linear_f64(x, w3, s3, 1, blk, N, rows=rows))
+    assert_parity(y[rows], ref, f"swiglu_released_{K}x{N}_blk{blk}")
