@@ -6,6 +6,7 @@ from ._lib import BiqError, InvalidArgument, Unsupported, version
 from .attention import (F16_STORAGE_F32_ACCUM, STRICT_F32, AttentionKernel,
                         NativeQ4FlashAttention, RmsNorm, attention,
                         effective_portable_query_chunk_size, qk_norm_rope)
+from .block import GqaAttention, RmsNormZero, SingleStreamBlock, block_glue
 from .linear import (Linear, LuminaFeedForward, linear_forward, q_matmul, q_matmul_swiglu,
                      qwen_linear_forward)
 from .q4 import (BOOGU_DENOISER, FLUX_VAE, QWEN3_VL, Q4Weight, from_packed,
@@ -22,5 +23,6 @@ __all__ = [
     "qwen_linear_forward", "Q4Weight", "from_packed",
     "q4s_storage_block_and_axis", "q4s_stored_dtype", "quantize_q4s_block128_f32",
     "quantize_row_layout_q4s_block_up_to128_f32", "BiqError", "InvalidArgument", "Unsupported",
+    "block_glue", "RmsNormZero", "GqaAttention", "SingleStreamBlock",
     "version", "BOOGU_DENOISER", "QWEN3_VL", "FLUX_VAE", "Q4_KN_AXIS1", "Q4_NK_AXIS0",
 ]

@@ -1,0 +1,143 @@
+// Row-wise glue of the modulated DiT block (crates/burn_boogu/src/model/block.rs:91-111) for
+// gfx950: strict-f32 RMS normalisation, tanh-gated residual update and (1 + scale) modulation,
+// fused so that each glue step reads and writes every activation row once.
+//
+//   r    = x + (branch / rms(branch)) * gamma_b * tanh(gate[b])       (x given: residual update)
+//   r    = branch                                                     (x NULL)
+//   next = ((r / rms(r)) * gamma_n) * (1 + scale[b])                  (next_out given)
+//
+// rms(v) = sqrt(mean(v^2) + eps) over the row, reduced in f32 (rms_normalized, norm.rs:28-35;
+// Burn's nn::RmsNorm for the gamma product; RmsNormZero's modulation order, norm.rs:144-152).
+// b = row / rows_per_batch picks the batch element's gate / scale row.  One 256-thread
+// workgroup per row; the row is read from global memory once per pass (the re-reads hit L2).
+#include <math.h>
+
+#include "common.h"
+
+namespace {
+
+constexpr int GT = 256;
+
+__device__ __forceinline__ float load_elem(const void *p, int dt, int64_t i) {
+  if (dt == BIQ_DTYPE_F32) return reinterpret_cast<const float *>(p)[i];
+  const uint16_t h = reinterpret_cast<const uint16_t *>(p)[i];
+  if (dt == BIQ_DTYPE_BF16) return biq::bitcast<float>((uint32_t)h << 16);
+  return biq::f16_bits_to_f32(h);
+}
+
+__device__ __forceinline__ void store_elem(void *p, int dt, int64_t i, float v) {
+  if (dt == BIQ_DTYPE_F32) reinterpret_cast<float *>(p)[i] = v;
+  else if (dt == BIQ_DTYPE_F16) reinterpret_cast<_Float16 *>(p)[i] = (_Float16)v;
+  else reinterpret_cast<uint16_t *>(p)[i] = (uint16_t)biq::f32_to_bf16_bits(v);
+}
+
+// Sum over the workgroup (all threads receive the result).
+__device__ __forceinline__ float block_sum(float v, float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();  // red may still be read by the previous reduction
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < GT / 64; ++i) t += red[i];
+  return t;
+}
+
+struct GlueArgs {
+  int64_t rows, width, rows_per_batch;
+  const float *x;
+  const void *branch;
+  int branch_dtype;
+  const float *branch_gamma;
+  float branch_eps;
+  const float *gate;
+  float *x_out;
+  const float *next_gamma;
+  float next_eps;
+  const float *next_scale;
+  void *next_out;
+  int next_dtype;
+};
+
+__global__ void __launch_bounds__(GT) block_glue_kernel(GlueArgs a) {
+  __shared__ float red[GT / 64];
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / a.rows_per_batch;
+  const int64_t W = a.width, base = row * W;
+  const float inv_w = 1.0f / (float)W;
+
+  // residual branch: r = x + branch / rms(branch) * gamma * tanh(gate), or r = branch
+  float rms_b = 1.0f;
+  if (a.x) {
+    float ss = 0.0f;
+    for (int64_t i = threadIdx.x; i < W; i += GT) {
+      const float v = load_elem(a.branch, a.branch_dtype, base + i);
+      ss += v * v;
+    }
+    rms_b = sqrtf(block_sum(ss, red) * inv_w + a.branch_eps);
+  }
+  float ss_r = 0.0f;
+  for (int64_t i = threadIdx.x; i < W; i += GT) {
+    const float v = load_elem(a.branch, a.branch_dtype, base + i);
+    float r = v;
+    if (a.x) {
+      float nb = v / rms_b;
+      if (a.branch_gamma) nb *= a.branch_gamma[i];
+      if (a.gate) nb *= tanhf(a.gate[b * W + i]);
+      r = a.x[base + i] + nb;
+      if (a.x_out) a.x_out[base + i] = r;
+    }
+    ss_r += r * r;
+  }
+  if (!a.next_out) return;
+  const float rms_r = sqrtf(block_sum(ss_r, red) * inv_w + a.next_eps);
+  // The residual row was written above by this same thread for the same i, so reading it back
+  // (or recomputing from the inputs when x_out is absent) gives the identical f32 value.
+  for (int64_t i = threadIdx.x; i < W; i += GT) {
+    float r;
+    if (a.x) {
+      if (a.x_out) {
+        r = a.x_out[base + i];
+      } else {
+        float nb = load_elem(a.branch, a.branch_dtype, base + i) / rms_b;
+        if (a.branch_gamma) nb *= a.branch_gamma[i];
+        if (a.gate) nb *= tanhf(a.gate[b * W + i]);
+        r = a.x[base + i] + nb;
+      }
+    } else {
+      r = load_elem(a.branch, a.branch_dtype, base + i);
+    }
+    float n = r / rms_r;
+    if (a.next_gamma) n *= a.next_gamma[i];
+    if (a.next_scale) n *= a.next_scale[b * W + i] + 1.0f;
+    store_elem(a.next_out, a.next_dtype, base + i, n);
+  }
+}
+
+}  // namespace
+
+extern "C" int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t rows_per_batch,
+                              const float *x, const void *branch, int branch_dtype,
+                              const float *branch_gamma, float branch_eps, const float *gate,
+                              float *x_out, const float *next_gamma, float next_eps,
+                              const float *next_scale, void *next_out, int next_dtype) {
+  biq::clear_error();
+  if (!branch) return biq::fail(BIQ_ERR_INVALID_ARG, "null branch");
+  if (rows <= 0 || width <= 0 || rows_per_batch <= 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "block glue requires non-empty rows, width and rows per batch");
+  if (rows > 0x7fffffffLL) return biq::fail(BIQ_ERR_UNSUPPORTED, "block glue: too many rows");
+  auto dt_ok = [](int d) { return d == BIQ_DTYPE_F32 || d == BIQ_DTYPE_F16 || d == BIQ_DTYPE_BF16; };
+  if (!dt_ok(branch_dtype) || (next_out && !dt_ok(next_dtype)))
+    return biq::fail(BIQ_ERR_INVALID_ARG, "block glue dtypes must be F32, F16 or BF16");
+  if (!x && !next_out) return biq::fail(BIQ_ERR_INVALID_ARG, "block glue has nothing to write");
+  if (x && !x_out && !next_out) return biq::fail(BIQ_ERR_INVALID_ARG, "block glue has nothing to write");
+  if (!(branch_eps >= 0.0f) || !(next_eps >= 0.0f))
+    return biq::fail(BIQ_ERR_INVALID_ARG, "block glue epsilons must be non-negative");
+  GlueArgs a{rows, width, rows_per_batch, x, branch, branch_dtype, branch_gamma, branch_eps, gate,
+             x_out, next_gamma, next_eps, next_scale, next_out, next_dtype};
+  hipLaunchKernelGGL(block_glue_kernel, dim3((unsigned)rows), dim3(GT), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return biq::check_launch("block glue");
+}
