@@ -94,13 +94,6 @@ __device__ __forceinline__ void f32x8_to_f16_split_slots(const float4 &a, const 
   }
 }
 
-template <int LAYOUT>
-__device__ __forceinline__ float load_scale(const float *__restrict__ scales, int64_t b, int64_t n,
-                                            int64_t N, int64_t nblk) {
-  if (n >= N || b >= nblk) return 0.0f;
-  return LAYOUT == BIQ_Q4_KN_AXIS1 ? scales[b * N + n] : scales[n * nblk + b];
-}
-
 // Tile geometry: a wave owns WM x WN MFMA tiles of 32 x 32; the workgroup holds WAVES_M x WAVES_N
 // waves.
 template <int WM_, int WN_, int WAVES_M_, int WAVES_N_, int BK_>
@@ -224,6 +217,16 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   };
   // Word rows of the [N, K/8] layout are 16-byte aligned only when K % 32 == 0.
   const bool vec_nk = (KW & 3) == 0;
+  // Block scales also come in through buffer loads: a scale outside the matrix reads as zero
+  // through an out-of-range offset.  (A select on the loaded value would make the wave wait for
+  // the whole prefetch right after issuing it.)
+  const auto rs = rsrc(scales, nblk * N * 4);
+  const auto rs3 = rsrc(GLU ? scales3 : scales, nblk * N * 4);
+  auto scale_off = [&](int64_t b, int j) -> uint32_t {
+    const int64_t n = ncol[j];
+    if (n >= N || b >= nblk) return OOB;
+    return (uint32_t)((LAYOUT == BIQ_Q4_KN_AXIS1 ? b * N + n : n * nblk + b) * 4);
+  };
 
   auto load_tile = [&](int64_t kt, TileRegs<G, XMODE> &R, float (&sc)[WN][TILE_BLOCKS]) {
     const auto ra = rsrc(reinterpret_cast<const char *>(xv) + (m0 * ldx + kt) * XSZ,
@@ -278,7 +281,8 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int t = 0; t < TILE_BLOCKS; ++t)
-        sc[j][t] = load_scale<LAYOUT>(GLU && j == 1 ? scales3 : scales, kt / BLK + t, ncol[j], N, nblk);
+        sc[j][t] = biq::bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(
+            GLU && j == 1 ? rs3 : rs, scale_off(kt / BLK + t, j), 0, 0));
   };
 
   // ---- registers -> LDS buffer (activation conversion to f16 slot order happens here)
@@ -334,7 +338,7 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   float sc[WN][TILE_BLOCKS], sc_next[WN][TILE_BLOCKS];
   load_tile(0, R, sc);
   store_tile(R, 0);
-  if (BK < K) load_tile(BK, R, sc_next);
+  load_tile(BK, R, sc_next);
   __syncthreads();
 
   int buf = 0;
@@ -356,14 +360,16 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
       for (int j = 0; j < WN; ++j)
 #pragma unroll
         for (int t = 0; t < TILE_BLOCKS; ++t) sc_cur[j][t] = sc[j][t];
-      if (has_next) {
-        store_tile(R, buf ^ 1);
+      // Staging and prefetch run unconditionally: past the end of K the buffer loads return
+      // zeros and the last tile's store lands in a buffer nobody reads again.  (A branch here
+      // makes the compiler merge the freshly loaded registers at the join, which waits for the
+      // whole prefetch before the first MFMA.)
+      store_tile(R, buf ^ 1);
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
+      for (int j = 0; j < WN; ++j)
 #pragma unroll
-          for (int t = 0; t < TILE_BLOCKS; ++t) sc[j][t] = sc_next[j][t];
-        if (kt + 2 * BK < K) load_tile(kt + 2 * BK, R, sc_next);
-      }
+        for (int t = 0; t < TILE_BLOCKS; ++t) sc[j][t] = sc_next[j][t];
+      load_tile(kt + 2 * BK, R, sc_next);
 #pragma unroll
       for (int j = 0; j < WN; ++j) b_cur[j] = unpack_q4_f16(w_cur[j]);
 
