@@ -192,8 +192,9 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
   auto rsrc = [&](const InT *base, int64_t kv0, int64_t row_b) {
     // valid offsets stay below 2^31 (host check), so capping the range there keeps OOB
     // offsets out of range for any sequence length
+    // A prefetch past the last key (kv0 >= Skv) gets an empty range: every load reads zero.
     const int64_t rem = (p.Skv - kv0) * row_b;
-    const uint32_t n = rem > 0x7fffffffLL ? 0x7fffffffu : (uint32_t)rem;
+    const uint32_t n = rem > 0x7fffffffLL ? 0x7fffffffu : (rem < 0 ? 0u : (uint32_t)rem);
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<InT *>(base + kv0 * (row_b / ESZ)), 0,
                                              (int)n, 0x00020000);
   };
@@ -213,12 +214,11 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
     const auto rk = rsrc(kg, kv0, krow_b);
 #pragma unroll
     for (int it = 0; it < K_CHUNKS; ++it) R.k16[it] = load16(rk, koff[it]);
-    // V: thread owns keys 4 kb .. 4 kb + 3 at dims d0 .. d0 + 7 (key-consecutive lanes)
-    if (tid < V_GROUPS) {
-      const auto rv = rsrc(vg, kv0, vrow_b);
+    // V: thread owns keys 4 kb .. 4 kb + 3 at dims d0 .. d0 + 7 (key-consecutive lanes);
+    // threads past V_GROUPS hold out-of-range offsets, so the loads need no branch
+    const auto rv = rsrc(vg, kv0, vrow_b);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) R.v16[j] = load16(rv, voff[j]);
-    }
+    for (int j = 0; j < 4; ++j) R.v16[j] = load16(rv, voff[j]);
   };
 
   // ---- registers -> LDS buffer: K row-major in the compute type, V transposed f16
@@ -270,8 +270,11 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
   __syncthreads();
 
   for (int64_t kv0 = kv_begin; kv0 < kv_end; kv0 += BKV, buf ^= 1) {
-    const bool has_next = kv0 + BKV < kv_end;
-    if (has_next) load_tile(kv0 + BKV, R);
+    // The next tile's loads and LDS stores run unconditionally: past the key range the buffer
+    // loads return zeros and the last store lands in a buffer nobody reads again.  (A branch
+    // here makes the compiler merge the prefetched registers at the join, which waits for the
+    // whole prefetch before the first MFMA.)
+    load_tile(kv0 + BKV, R);
 
     // ---- S^T = K Q^T for the tile's 64 keys (2 x 32)
     floatx16_t sacc[2];
@@ -360,7 +363,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
       }
     }
 
-    if (has_next) store_tile(R, buf ^ 1);
+    store_tile(R, buf ^ 1);
     __syncthreads();
   }
 
