@@ -196,3 +196,30 @@ def test_gpu_execute_gqa_with_qk_norm_rope_matches_composition(gpu, oracle):
             B.RmsNorm(dev(gq, device=gpu)), B.RmsNorm(dev(gk, device=gpu)),
             (dev(cos[None], device=gpu), dev(sin[None], device=gpu)), 8192,
             rms_norm_policy=B.F16_STORAGE_F32_ACCUM)
+
+
+@pytest.mark.parametrize("odt", [torch.float32, torch.bfloat16])
+def test_gpu_many_items_ragged_keys(gpu, oracle, odt):
+    """600 query blocks (more than one resident round of workgroups), ragged keys (S = 1800, not
+    a multiple of the 64-key tile, so the last tile's prefetch runs past the sequence), D = 120,
+    GQA 40:10; sampled rows of every head against the f64 oracle and every element against an
+    fp32 reference; bit-identical on a repeat call."""
+    rng = np.random.default_rng(44)
+    Bn, H, Hkv, S, D = 1, 40, 10, 1800, 120
+    q = W.round_to_bf16(rng.standard_normal((Bn, H, S, D)).astype(np.float32))
+    k = W.round_to_bf16(rng.standard_normal((Bn, Hkv, S, D)).astype(np.float32))
+    v = W.round_to_bf16(rng.standard_normal((Bn, Hkv, S, D)).astype(np.float32))
+    qd, kd, vd = (dev(a, torch.bfloat16, gpu) for a in (q, k, v))
+    out = B.attention(qd, kd, vd, out_dtype=odt)
+    assert torch.equal(out, B.attention(qd, kd, vd, out_dtype=odt))
+    rows = sample_rows(S, n=20, seed=44)
+    ref = oracle.attention_f64(q, k, v, rows=rows).astype(np.float32)
+    got = host(out[:, :, torch.from_numpy(rows).to(gpu)])
+    if odt == torch.float32:
+        assert_parity(got, ref, "many_items_sampled")
+        kx = kd.repeat_interleave(H // Hkv, dim=1).contiguous()
+        vx = vd.repeat_interleave(H // Hkv, dim=1).contiguous()
+        full = torch_fp32_attention(qd, kx, vx, 1.0 / np.sqrt(D))
+        assert_parity(host(out), host(full), "many_items_full_vs_fp32")
+    else:
+        assert np.max(np.abs(got - ref)) <= np.max(np.abs(ref)) * 2.0 ** -7 + 2e-3
