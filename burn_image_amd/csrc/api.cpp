@@ -56,6 +56,20 @@ int stream_workspace(hipStream_t s, size_t bytes, void **out) {
   return BIQ_OK;
 }
 
+int device_cu_count() {
+  static std::mutex m;
+  static std::map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(m);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+  cache[dev] = n;
+  return n;
+}
+
 }  // namespace biq
 
 extern "C" {

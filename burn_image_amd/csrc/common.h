@@ -32,6 +32,8 @@ int fail(int status, const std::string &msg);
 int check_launch(const char *what);
 // Device scratch owned by the library for (current device, stream s), at least `bytes` long.
 int stream_workspace(hipStream_t s, size_t bytes, void **out);
+// Compute units of the current device.
+int device_cu_count();
 
 // ---------------------------------------------------------------------------------------------
 // device helpers

@@ -25,6 +25,8 @@
 // into the other LDS buffer afterwards, so one barrier per tile separates the two.  Workgroups are
 // numbered so that each XCD (hardware places workgroup i on XCD i % 8) walks a compact,
 // M-grouped block of output tiles, keeping the shared activation and weight tiles in its L2.
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace {
@@ -130,6 +132,105 @@ struct TileRegs {
   u32x4_t b[G::B_CHUNKS];
 };
 
+// Work split of one launch.  Workgroups [0, dp_tiles) each own one whole output tile (in the
+// XCD-aware order below).  When whole-tile rounds would leave the last round mostly idle, the
+// remaining tail tiles are split along K into `parts` equal runs of K units (one unit = the K of
+// one outer iteration, whole quantisation blocks): chunk c is part c / tail of tail tile
+// c % tail, and tail workgroup w computes chunks w, w + sk_wgs, ...  All chunks in flight at a
+// time then cover the same K range of neighbouring tiles (the activation and weight tiles they
+// read are shared in L2, as for owned tiles).  A chunk writes its partial accumulators to slot c
+// of `part`; a second kernel (q4_tail_reduce_kernel) adds each tile's partials in K order and
+// applies the epilogue, so the result does not depend on which chunk finished first.
+struct SkPlan {
+  int dp_tiles;
+  int sk_wgs;     // 0: every tile is owned
+  int parts;      // K parts of a tail tile
+  int64_t units;  // K units per tile
+  float *part;    // (tiles - dp_tiles) * parts partial tiles of BM x BN f32, register-major
+};
+
+// pid -> output tile: M-grouped raster (GROUP_M M tiles per group, walked column by column).
+__device__ __forceinline__ void tile_coords(int64_t pid, int tiles_m, int tiles_n, int64_t &tile_m,
+                                            int64_t &tile_n) {
+  const int64_t in_group = (int64_t)GROUP_M * tiles_n;
+  const int64_t first_m = (pid / in_group) * GROUP_M;
+  const int64_t gsize = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
+  tile_m = first_m + (pid % in_group) % gsize;
+  tile_n = (pid % in_group) / gsize;
+}
+
+// Epilogue of one wave's accumulators, registers r in [r_lo, r_hi) of each 32 x 32 tile: bias
+// (or the SwiGLU gate), conversion, store.  Register r of MFMA tile (i, j) holds row
+// 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4 and column 32 j + lane % 32 of the wave tile.
+template <class G, bool GLU>
+__device__ __forceinline__ void store_tile_out(const floatx16_t (&acc)[G::WM][G::WN], int64_t m0,
+                                               int64_t n0, const float *__restrict__ bias,
+                                               void *__restrict__ yv, int y_dtype, int64_t M,
+                                               int64_t N, int r_lo, int r_hi) {
+  constexpr int WM = G::WM, WN = G::WN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
+  const int l32 = lane & 31, lh = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < (GLU ? 1 : WN); ++j) {
+    const int64_t col = GLU ? n0 + wn * 32 + l32 : n0 + wn * (32 * WN) + 32 * j + l32;
+    if (col >= N) continue;
+    const float bv = (!GLU && bias) ? bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if (r < r_lo || r >= r_hi) continue;
+        const int64_t row = m0 + wm * (32 * WM) + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (row >= M) continue;
+        float v = acc[i][j][r] + bv;
+        if constexpr (GLU) {
+          // silu(a) = a / (1 + e^-a), times the W3 projection of the same row and column
+          v = v / (1.0f + __expf(-v)) * acc[i][1][r];
+        }
+        if (y_dtype == BIQ_DTYPE_F32) {
+          reinterpret_cast<float *>(yv)[row * N + col] = v;
+        } else if (y_dtype == BIQ_DTYPE_F16) {
+          reinterpret_cast<_Float16 *>(yv)[row * N + col] = (_Float16)v;
+        } else {
+          reinterpret_cast<uint16_t *>(yv)[row * N + col] = (uint16_t)biq::f32_to_bf16_bits(v);
+        }
+      }
+  }
+}
+
+// Tail reduction: workgroup (tile t, register group g) adds the `parts` partials of tail tile t
+// in K order for registers [4 g, 4 g + 4) of every MFMA tile and writes those outputs.
+template <class G, bool GLU>
+__global__ void __launch_bounds__(G::NTHREADS)
+    q4_tail_reduce_kernel(const float *__restrict__ part, int tail, int parts, int dp_tiles,
+                          int tiles_m, int tiles_n, const float *__restrict__ bias,
+                          void *__restrict__ yv, int y_dtype, int64_t M, int64_t N) {
+  constexpr int WM = G::WM, WN = G::WN, NT = G::NTHREADS, PART = G::BM * G::BN, RG = 4;
+  constexpr int BNO = GLU ? G::BN / 2 : G::BN;
+  const int64_t t = blockIdx.x / (16 / RG);
+  const int r_lo = (int)(blockIdx.x % (16 / RG)) * RG;
+  const int tid = threadIdx.x;
+  int64_t tile_m, tile_n;
+  tile_coords(dp_tiles + t, tiles_m, tiles_n, tile_m, tile_n);
+  floatx16_t acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[i][j] = biq::zero16();
+  for (int p = 0; p < parts; ++p) {
+    const float *src = part + ((int64_t)p * tail + t) * PART;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < RG; ++r)
+          acc[i][j][r_lo + r] += src[((i * WN + j) * 16 + r_lo + r) * NT + tid];
+  }
+  store_tile_out<G, GLU>(acc, tile_m * G::BM, tile_n * BNO, bias, yv, y_dtype, M, N, r_lo, r_lo + RG);
+}
+
 // GLU: the SwiGLU form y = silu(x . W1) * (x . W3) of the reference's feed-forward
 // (crates/burn_boogu/src/model/feed_forward.rs:32-36).  A workgroup then covers BN / 2 output
 // columns of both weights: the word tile holds W1's columns in its first half and W3's in its
@@ -141,7 +242,7 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
                    const float *__restrict__ scales, const uint32_t *__restrict__ words3,
                    const float *__restrict__ scales3, const float *__restrict__ bias,
                    void *__restrict__ yv, int y_dtype, int64_t M, int64_t N, int64_t K,
-                   int tiles_m, int tiles_n) {
+                   int tiles_m, int tiles_n, SkPlan sk) {
   constexpr int WM = G::WM, WN = G::WN, BM = G::BM, BN = G::BN, NT = G::NTHREADS;
   static_assert(!GLU || WN == 2, "the SwiGLU form pairs the two column tiles of a wave");
   constexpr int BNO = GLU ? BN / 2 : BN;  // output columns per workgroup
@@ -158,19 +259,33 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
   const int l32 = lane & 31, lh = lane >> 5;
 
-  // ---- XCD-aware, M-grouped tile order
-  int64_t pid;
-  {
-    const int64_t T = (int64_t)tiles_m * tiles_n;
-    const int64_t L = blockIdx.x;
-    const int64_t q = T / 8, r = T % 8, xcd = L % 8, slot = L / 8;
-    pid = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
-  }
-  const int64_t in_group = (int64_t)GROUP_M * tiles_n;
-  const int64_t first_m = (pid / in_group) * GROUP_M;
-  const int64_t gsize = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
-  const int64_t tile_m = first_m + (pid % in_group) % gsize;
-  const int64_t tile_n = (pid % in_group) / gsize;
+  // ---- this workgroup's tile segments.  Owned tiles come in the XCD-aware order: hardware
+  //      places workgroup L on XCD L % 8, and the workgroups of one XCD take a compact run of
+  //      pids (tail workgroups likewise take a compact run of chunk indices; dp_tiles is a
+  //      multiple of 8, so tail workgroup w also runs on XCD w % 8).
+  const int64_t T = (int64_t)tiles_m * tiles_n;
+  const int64_t L = blockIdx.x;
+  const int64_t units = sk.units;
+  const bool tail_wg = L >= sk.dp_tiles;
+  const int64_t tail = T - sk.dp_tiles, chunks = tail * sk.parts;
+  auto xcd_order = [](int64_t i, int64_t n) {
+    const int64_t q = n / 8, r = n % 8, xcd = i % 8, slot = i / 8;
+    return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+  };
+  const int64_t first = tail_wg ? xcd_order(L - sk.dp_tiles, sk.sk_wgs) : xcd_order(L, sk.dp_tiles);
+  const int64_t n_seg = tail_wg ? (chunks - first + sk.sk_wgs - 1) / sk.sk_wgs : 1;
+
+  for (int64_t seg = 0; seg < n_seg; ++seg) {
+  const int64_t c = first + seg * sk.sk_wgs;  // tail chunk (tail workgroups only)
+  const int64_t t_tail = tail_wg ? c % tail : 0, k_part = tail_wg ? c / tail : 0;
+  const int64_t pid = tail_wg ? sk.dp_tiles + t_tail : first;
+  const int64_t ku0 = tail_wg ? k_part * units / sk.parts : 0;
+  const int64_t ku1 = tail_wg ? (k_part + 1) * units / sk.parts : units;
+  constexpr int64_t UNIT = (int64_t)TPB * BK;
+  const int64_t k_lo = ku0 * UNIT, k_hi = ku1 * UNIT < K ? ku1 * UNIT : K;
+
+  int64_t tile_m, tile_n;
+  tile_coords(pid, tiles_m, tiles_n, tile_m, tile_n);
   const int64_t m0 = tile_m * BM, n0 = tile_n * BNO;
   const int64_t nblk = K / BLK;
   const int64_t KW = K / 8;
@@ -336,16 +451,16 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   // and the loads of tile t+2 are issued right after, a whole tile ahead of their use.
   TileRegs<G, XMODE> R;
   float sc[WN][TILE_BLOCKS], sc_next[WN][TILE_BLOCKS];
-  load_tile(0, R, sc);
+  load_tile(k_lo, R, sc);
   store_tile(R, 0);
-  load_tile(BK, R, sc_next);
+  load_tile(k_lo + BK, R, sc_next);
   __syncthreads();
 
   int buf = 0;
   // Outer iterations cover whole quantisation blocks (or one K tile of several small blocks),
   // so the first / last step of every block is known at compile time: the MFMA chain of a block
   // starts from an inline zero and no accumulator is copied or selected at run time.
-  for (int64_t kg = 0; kg < K; kg += TPB * BK) {
+  for (int64_t kg = k_lo; kg < k_hi; kg += UNIT) {
 #pragma unroll
     for (int tt = 0; tt < TPB; ++tt) {
       const int64_t kt = kg + tt * BK;
@@ -433,31 +548,25 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   }
 
   // ---------------- epilogue: bias (or the SwiGLU gate), convert, store ---------------------
-#pragma unroll
-  for (int j = 0; j < (GLU ? 1 : WN); ++j) {
-    const int64_t col = ncol[j];
-    if (col >= N) continue;
-    const float bv = (!GLU && bias) ? bias[col] : 0.0f;
+  if (ku0 == 0 && ku1 == units) {  // the whole K of the tile
+    store_tile_out<G, GLU>(acc, m0, n0, bias, yv, y_dtype, M, N, 0, 16);
+    continue;
+  }
+  // ---- tail chunk: the partial goes to slot c, register-major (element (register q, thread
+  //      tid) at q * NT + tid: one coalesced 256-byte row per wave and register)
+  {
+    constexpr int PART = BM * BN;
+    const auto dst = __builtin_amdgcn_make_buffer_rsrc(sk.part + c * PART, 0, PART * 4, 0x00020000);
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * (32 * WM) + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (row >= M) continue;
-        float v = acc[i][j][r] + bv;
-        if constexpr (GLU) {
-          // silu(a) = a / (1 + e^-a), times the W3 projection of the same row and column
-          v = v / (1.0f + __expf(-v)) * acc[i][1][r];
-        }
-        if (y_dtype == BIQ_DTYPE_F32) {
-          reinterpret_cast<float *>(yv)[row * N + col] = v;
-        } else if (y_dtype == BIQ_DTYPE_F16) {
-          reinterpret_cast<_Float16 *>(yv)[row * N + col] = (_Float16)v;
-        } else {
-          reinterpret_cast<uint16_t *>(yv)[row * N + col] = (uint16_t)biq::f32_to_bf16_bits(v);
-        }
-      }
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          __builtin_amdgcn_raw_buffer_store_b32(biq::bitcast<uint32_t>(acc[i][j][r]), dst, tid * 4,
+                                                ((i * WN + j) * 16 + r) * NT * 4, 0);
   }
+  }  // segments
 }
 
 // Weights of one launch: W (and W3 for the SwiGLU form).
@@ -466,29 +575,78 @@ struct Q4Args {
   const float *scales, *scales3;
 };
 
+// Split of a grid of T tiles of `units` K units each over `cus` compute units (see SkPlan): the
+// whole rounds are owned tiles; the tail of T % cus tiles is split into the number of K parts
+// that minimises the estimated time, counted in tile times: rounds of chunks, each chunk 1 /
+// parts of a tile plus the cost of writing and reading back a round of partials (~0.13 tile),
+// plus the tail reduction's read of a tile's partials (~0.012 tile per part).  A tail that is
+// already most of a round stays whole.
+SkPlan plan_tail(int64_t T, int64_t units, int cus) {
+  SkPlan p{(int)T, 0, 1, units, nullptr};
+  const char *env = getenv("BIQ_GEMM_STREAMK");
+  if (cus <= 0 || units < 2 || (env && env[0] == '0')) return p;
+  const int64_t tail = T % cus;
+  if (tail == 0) return p;
+  double best = 1.0;
+  int parts = 1;
+  for (int s = 2; s <= 16 && s <= units; ++s) {
+    const int64_t rounds = (tail * s + cus - 1) / cus;
+    const double est = rounds * (1.0 / s + 0.13) + 0.012 * s;
+    if (est < best - 0.05) {
+      best = est;
+      parts = s;
+    }
+  }
+  if (parts == 1) return p;
+  p.dp_tiles = (int)(T - tail);
+  p.parts = parts;
+  p.sk_wgs = (int)(tail * parts < cus ? tail * parts : cus);
+  return p;
+}
+
+template <class GG, int LAYOUT, int XMODE, int B, bool GLU>
+int launch_geo(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const float *bias,
+               void *y, int y_dtype, int64_t M, int64_t N, int64_t K) {
+  constexpr int BNO = GLU ? GG::BN / 2 : GG::BN;
+  constexpr int64_t UNIT = (int64_t)(B >= GG::BK ? B : GG::BK);
+  const int tiles_m = (int)((M + GG::BM - 1) / GG::BM), tiles_n = (int)((N + BNO - 1) / BNO);
+  const int64_t T = (int64_t)tiles_m * tiles_n;
+  SkPlan plan = plan_tail(T, (K + UNIT - 1) / UNIT, biq::device_cu_count());
+  const int tail = (int)(T - plan.dp_tiles);
+  if (plan.sk_wgs > 0) {
+    void *part = nullptr;
+    const size_t chunks = (size_t)tail * plan.parts;
+    const int st = biq::stream_workspace(s, chunks * GG::BM * GG::BN * sizeof(float), &part);
+    if (st != BIQ_OK) return st;
+    plan.part = reinterpret_cast<float *>(part);
+  }
+  dim3 grid((unsigned)(plan.dp_tiles + plan.sk_wgs));
+  hipLaunchKernelGGL((q4_gemm_kernel<GG, LAYOUT, XMODE, B, GLU>), grid, dim3(GG::NTHREADS), 0, s, x,
+                     ldx, w.words, w.scales, w.words3, w.scales3, bias, y, y_dtype, M, N, K,
+                     tiles_m, tiles_n, plan);
+  if (plan.sk_wgs > 0) {
+    const int st = biq::check_launch(GLU ? "q4 linear swiglu" : "q4 linear");
+    if (st != BIQ_OK) return st;
+    hipLaunchKernelGGL((q4_tail_reduce_kernel<GG, GLU>), dim3((unsigned)tail * 4), dim3(GG::NTHREADS),
+                       0, s, plan.part, tail, plan.parts, plan.dp_tiles, tiles_m, tiles_n, bias, y,
+                       y_dtype, M, N);
+  }
+  return biq::check_launch(GLU ? "q4 linear swiglu" : "q4 linear");
+}
+
 template <int LAYOUT, int XMODE, bool GLU>
 int launch_blk(hipStream_t s, int block, const void *x, int64_t ldx, const Q4Args &w,
                const float *bias, void *y, int y_dtype, int64_t M, int64_t N, int64_t K) {
   using G8 = GemmGeo<XMODE, 8>;
   using G16 = GemmGeo<XMODE, 16>;
   using G = GemmGeo<XMODE, 128>;
-  constexpr int BNO = GLU ? G::BN / 2 : G::BN;
-  const int tiles_m = (int)((M + G::BM - 1) / G::BM), tiles_n = (int)((N + BNO - 1) / BNO);
-  dim3 grid((unsigned)((int64_t)tiles_m * tiles_n));
-  dim3 blk(G::NTHREADS);
-#define BIQ_LAUNCH(GG, B)                                                                          \
-  hipLaunchKernelGGL((q4_gemm_kernel<GG, LAYOUT, XMODE, B, GLU>), grid, blk, 0, s, x, ldx,        \
-                     w.words, w.scales, w.words3, w.scales3, bias, y, y_dtype, M, N, K, tiles_m,  \
-                     tiles_n)
   switch (block) {
-    case 8: BIQ_LAUNCH(G8, 8); break;
-    case 16: BIQ_LAUNCH(G16, 16); break;
-    case 32: BIQ_LAUNCH(G, 32); break;
-    case 64: BIQ_LAUNCH(G, 64); break;
-    default: BIQ_LAUNCH(G, 128); break;
+    case 8: return launch_geo<G8, LAYOUT, XMODE, 8, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K);
+    case 16: return launch_geo<G16, LAYOUT, XMODE, 16, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K);
+    case 32: return launch_geo<G, LAYOUT, XMODE, 32, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K);
+    case 64: return launch_geo<G, LAYOUT, XMODE, 64, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K);
+    default: return launch_geo<G, LAYOUT, XMODE, 128, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K);
   }
-#undef BIQ_LAUNCH
-  return biq::check_launch(GLU ? "q4 linear swiglu" : "q4 linear");
 }
 
 template <int LAYOUT, bool GLU>

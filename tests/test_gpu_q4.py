@@ -133,9 +133,12 @@ def sample_rows(M, n=40, seed=0):
 
 
 @pytest.mark.parametrize("name", list(W.C3_SHAPES))
-def test_gpu_c3_projection_full_shape(gpu, oracle, name):
+def test_gpu_c3_projection_full_shape(gpu, oracle, name, monkeypatch):
     """C3 at M = 4608: sampled rows against the float64 oracle; every element against an fp32
-    product of the (bit-exact) dequantised weight; row-permutation equivariance bit-exact."""
+    product of the (bit-exact) dequantised weight; row-permutation equivariance.  Rows of a tail
+    tile whose K is split between workgroups are summed in another order than rows of a tile one
+    workgroup owns, so under a row permutation the output is equal within the parity gate; with
+    the split switched off (every tile owned) it is bit-exact."""
     K, N = W.C3_SHAPES[name]
     M = 4608
     idx = list(W.C3_SHAPES).index(name)
@@ -152,7 +155,11 @@ def test_gpu_c3_projection_full_shape(gpu, oracle, name):
     assert_parity(host(y), host(full_ref), f"c3_{name}_full_vs_fp32")
     perm = torch.randperm(M, generator=torch.Generator().manual_seed(idx)).to(gpu)
     y_perm = B.q_matmul(xd[perm].contiguous(), q)
-    assert torch.equal(y_perm, y[perm])
+    assert_parity(host(y_perm), host(y[perm]), f"c3_{name}_row_permutation", max_abs=1e-4, mean_rel=1e-6)
+    monkeypatch.setenv("BIQ_GEMM_STREAMK", "0")
+    y_owned = B.q_matmul(xd, q)
+    assert_parity(host(y_owned), host(y), f"c3_{name}_owned_tiles", max_abs=1e-4, mean_rel=1e-6)
+    assert torch.equal(B.q_matmul(xd[perm].contiguous(), q), y_owned[perm])
 
 
 @pytest.mark.parametrize("name", list(W.C5_SHAPES))
@@ -257,6 +264,53 @@ def test_gpu_q4_linear_small_m_deterministic_and_graph_replay(gpu, oracle):
         torch.cuda.synchronize()
         assert torch.equal(out, y0), f"replay {i}"
         B.q_matmul(xd[:1], q)  # unrelated eager work between replays
+
+
+@pytest.mark.parametrize("M,K,N,block,xdt,glu", [
+    (4608, 3072, 9216, 128, "bf16", False),  # 1296 tiles: a tail of 16 tiles in 6 K parts
+    (4608, 1024, 12288, 128, "bf16", True),  # SwiGLU, 3456 tiles: a tail of 128 in 2 parts
+    (300, 1024, 1000, 32, "f16", False),     # 12 ragged tiles, block 32
+    (300, 2048, 1000, 64, "bf16", True),     # SwiGLU, 24 ragged tiles, block 64
+    (256, 768, 512, 128, "f32", False),      # f32 activations: one K unit is two staged tiles
+    (200, 512, 256, 8, "bf16", False),       # block 8 (masked MFMA path)
+])
+def test_gpu_q4_linear_split_tail(gpu, oracle, monkeypatch, M, K, N, block, xdt, glu):
+    """Tail tiles split along K between workgroups: sampled rows against the float64 oracle, the
+    whole output against the every-tile-owned launch (same gate as any two summation orders),
+    repeated calls and graph replays (GEMM + tail reduction kernels) bitwise equal."""
+    x = W.activations(19, M + K, M, K, xdt)
+    words, scales = W.q4_weight(19, N, K, N, layout=1, block=block)
+    q = weight(words, scales, 1, block, K, N, gpu)
+    xd = dev(x, TORCH_DT[xdt], gpu)
+    rows = sample_rows(M, seed=M)
+    ref = oracle.q4_linear_f64(x, words, scales, 1, block, N, rows=rows).astype(np.float32)
+    if glu:
+        w3, s3 = W.q4_weight(19, N + 1, K, N, layout=1, block=block)
+        q3 = weight(w3, s3, 1, block, K, N, gpu)
+        ref = silu_gate_ref(ref, oracle.q4_linear_f64(x, w3, s3, 1, block, N, rows=rows).astype(np.float32))
+        call = lambda out=None: B.q_matmul_swiglu(xd, q, q3, out=out)  # noqa: E731
+    else:
+        call = lambda out=None: B.q_matmul(xd, q, out=out)  # noqa: E731
+    y = call()
+    assert_parity(host(y[torch.from_numpy(rows).to(gpu)]), ref, f"split_tail_{M}x{K}x{N}_blk{block}_{xdt}")
+    for _ in range(3):
+        assert torch.equal(call(), y)
+    stream = torch.cuda.Stream()
+    out = torch.zeros_like(y)
+    with torch.cuda.stream(stream):
+        call(out)  # sizes this stream's scratch outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        call(out)
+    for i in range(3):
+        out.fill_(float(i))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y), f"replay {i}"
+        call()  # eager work on the default stream between replays
+    monkeypatch.setenv("BIQ_GEMM_STREAMK", "0")
+    assert_parity(host(call()), host(y), "split_tail_vs_owned", max_abs=1e-4, mean_rel=1e-6)
 
 
 def silu_gate_ref(y1, y3):
