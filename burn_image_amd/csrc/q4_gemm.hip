@@ -124,12 +124,22 @@ struct Geo {
 template <int XMODE, int BLK>
 using GemmGeo = Geo<BIQ_GEMM_WAVES, (XMODE == XM_F32 || BLK <= 16) ? 64 : BIQ_GEMM_BK>;
 
+// Register sets of the global -> LDS pipeline (see the kernel): two for 16-bit activations,
+// blocks of 128 and the [K/8, N] word layout; one where a second set would not fit the 256
+// registers without spilling.
+template <int LAYOUT, int XMODE, int BLK>
+constexpr int PF_SETS = (LAYOUT == BIQ_Q4_KN_AXIS1 && XMODE != XM_F32 && BLK >= 128) ? 2 : 1;
+// K units a tail part starts on a multiple of (see the kernel's paired loop)
+template <int LAYOUT, int XMODE, int BLK, int BK>
+constexpr int PART_GRANULE = (PF_SETS<LAYOUT, XMODE, BLK> == 2 && BLK <= BK) ? 2 : 1;
+
 // Per-thread register copy of one tile's global data.
-template <class G, int XMODE>
+template <class G, int XMODE, int NSC>
 struct TileRegs {
   u32x4_t a16[XMODE == XM_F32 ? 1 : G::A_CHUNKS];
   float4 a32[XMODE == XM_F32 ? 2 * G::A_CHUNKS : 1];
   u32x4_t b[G::B_CHUNKS];
+  float sc[G::WN][NSC];  // block scales of this thread's columns
 };
 
 // Work split of one launch.  Workgroups [0, dp_tiles) each own one whole output tile (in the
@@ -250,7 +260,8 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   constexpr int B_LD = BN;  // LDS row stride of the word tile, in words
   constexpr int NSPLIT = XMODE == XM_F32 ? 2 : 1;
   constexpr int TILE_BLOCKS = BLK >= BK ? 1 : BK / BLK;
-  constexpr int TPB = BLK >= BK ? BLK / BK : 1;  // K tiles per outer iteration
+  constexpr int TPB = BLK >= BK ? BLK / BK : 1;  // K tiles per quantisation block
+  static_assert(TPB == 1 || TPB == 2, "a pair of K tiles must cover whole blocks");
   __shared__ __attribute__((aligned(16))) uint16_t As[2][NSPLIT][BM * A_LD];
   __shared__ __attribute__((aligned(16))) uint32_t Bs[2][(BK / 8) * B_LD];
 
@@ -279,8 +290,14 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   const int64_t c = first + seg * sk.sk_wgs;  // tail chunk (tail workgroups only)
   const int64_t t_tail = tail_wg ? c % tail : 0, k_part = tail_wg ? c / tail : 0;
   const int64_t pid = tail_wg ? sk.dp_tiles + t_tail : first;
-  const int64_t ku0 = tail_wg ? k_part * units / sk.parts : 0;
-  const int64_t ku1 = tail_wg ? (k_part + 1) * units / sk.parts : units;
+  // with two register sets, tail parts start on even K tiles, so every part but the last (which
+  // ends at K) has an even number of tiles for the paired loop below
+  constexpr int64_t GRAN = PART_GRANULE<LAYOUT, XMODE, BLK, G::BK>;
+  auto part_start = [&](int64_t kp) {
+    return kp >= sk.parts ? units : GRAN * (kp * (units / GRAN) / sk.parts);
+  };
+  const int64_t ku0 = tail_wg ? part_start(k_part) : 0;
+  const int64_t ku1 = tail_wg ? part_start(k_part + 1) : units;
   constexpr int64_t UNIT = (int64_t)TPB * BK;
   const int64_t k_lo = ku0 * UNIT, k_hi = ku1 * UNIT < K ? ku1 * UNIT : K;
 
@@ -309,14 +326,34 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     const int c = tid + it * NT;
     a_off[it] = (uint32_t)(((int64_t)(c / (BK / 8)) * ldx + 8 * (c % (BK / 8))) * XSZ);
   }
+  // GLU with an even number of word groups per thread: groups [0, B_CHUNKS / 2) come from W1
+  // and the rest from W3 (for the [N, K/8] layout the plain numbering already does this), so each
+  // load names its weight at compile time.  Otherwise both weights are read with the same offset,
+  // the other weight's lanes passing an out-of-range offset (zero, no memory access), and the
+  // two results are OR-ed -- which makes the wave wait for them right away.
+  constexpr bool GLU_SPLIT = GLU && G::B_CHUNKS % 2 == 0;
+  auto kn_group = [&](int it, int &kwr, int &nc, bool &w3) {  // [K/8, N] word group `it`
+    if constexpr (GLU_SPLIT) {
+      const int ch = tid + (it % (G::B_CHUNKS / 2)) * NT;
+      w3 = it >= G::B_CHUNKS / 2;
+      kwr = ch / (BNO / 4);
+      nc = (ch % (BNO / 4)) * 4;
+    } else {
+      const int c = tid + it * NT;
+      kwr = c / (BN / 4);
+      nc = (c % (BN / 4)) * 4;
+      w3 = GLU && nc >= BNO;
+      nc -= w3 ? BNO : 0;
+    }
+  };
 #pragma unroll
   for (int it = 0; it < G::B_CHUNKS; ++it) {
     const int c = tid + it * NT;
     if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
-      const int kwr = c / (BN / 4);
-      int nc = (c % (BN / 4)) * 4;
-      b_w3[it] = GLU && nc >= BNO;
-      nc -= b_w3[it] ? BNO : 0;
+      int kwr, nc;
+      bool w3;
+      kn_group(it, kwr, nc, w3);
+      b_w3[it] = w3;
       b_off[it] = n0 + nc < N ? (uint32_t)(((int64_t)kwr * N + nc) * 4) : OOB;
     } else {
       const int part4 = c % (BK / 32);
@@ -343,7 +380,14 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     return (uint32_t)((LAYOUT == BIQ_Q4_KN_AXIS1 ? b * N + n : n * nblk + b) * 4);
   };
 
-  auto load_tile = [&](int64_t kt, TileRegs<G, XMODE> &R, float (&sc)[WN][TILE_BLOCKS]) {
+  auto load_tile = [&](int64_t kt, TileRegs<G, XMODE, TILE_BLOCKS> &R) {
+    // scales first: a wait for the tile's data then covers them too
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int t = 0; t < TILE_BLOCKS; ++t)
+        R.sc[j][t] = biq::bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(
+            GLU && j == 1 ? rs3 : rs, scale_off(kt / BLK + t, j), 0, 0));
     const auto ra = rsrc(reinterpret_cast<const char *>(xv) + (m0 * ldx + kt) * XSZ,
                          ((M - m0) * ldx - kt) * XSZ);
 #pragma unroll
@@ -358,17 +402,17 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
       }
     }
     const int64_t kw0 = kt / 8;
-    // GLU: both weights are read with the same offsets; the lanes of the other weight pass an
-    // out-of-range offset (zero, no memory access) and the two results are OR-ed.
     auto ld128 = [&](const __amdgpu_buffer_rsrc_t &r1, const __amdgpu_buffer_rsrc_t &r3, uint32_t off,
-                     bool w3) -> u32x4_t {
+                     bool w3, int it) -> u32x4_t {
       if constexpr (!GLU) return __builtin_amdgcn_raw_buffer_load_b128(r1, off, 0, 0);
+      if constexpr (GLU_SPLIT) return __builtin_amdgcn_raw_buffer_load_b128(it >= G::B_CHUNKS / 2 ? r3 : r1, off, 0, 0);
       return __builtin_amdgcn_raw_buffer_load_b128(r1, w3 ? OOB : off, 0, 0) |
              __builtin_amdgcn_raw_buffer_load_b128(r3, w3 ? off : OOB, 0, 0);
     };
     auto ld32 = [&](const __amdgpu_buffer_rsrc_t &r1, const __amdgpu_buffer_rsrc_t &r3, uint32_t off,
-                    bool w3) -> uint32_t {
+                    bool w3, int it) -> uint32_t {
       if constexpr (!GLU) return __builtin_amdgcn_raw_buffer_load_b32(r1, off, 0, 0);
+      if constexpr (GLU_SPLIT) return __builtin_amdgcn_raw_buffer_load_b32(it >= G::B_CHUNKS / 2 ? r3 : r1, off, 0, 0);
       return __builtin_amdgcn_raw_buffer_load_b32(r1, w3 ? OOB : off, 0, 0) |
              __builtin_amdgcn_raw_buffer_load_b32(r3, w3 ? off : OOB, 0, 0);
     };
@@ -376,7 +420,7 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
       const auto rb = rsrc(words + kw0 * N + n0, ((KW - kw0) * N - n0) * 4);
       const auto rb3 = rsrc((GLU ? words3 : words) + kw0 * N + n0, ((KW - kw0) * N - n0) * 4);
 #pragma unroll
-      for (int it = 0; it < G::B_CHUNKS; ++it) R.b[it] = ld128(rb, rb3, b_off[it], b_w3[it]);
+      for (int it = 0; it < G::B_CHUNKS; ++it) R.b[it] = ld128(rb, rb3, b_off[it], b_w3[it], it);
     } else {
       const auto rb = rsrc(words + n0 * KW + kw0, ((N - n0) * KW - kw0) * 4);
       const auto rb3 = rsrc((GLU ? words3 : words) + n0 * KW + kw0, ((N - n0) * KW - kw0) * 4);
@@ -385,23 +429,17 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
         const int part4 = (tid + it * NT) % (BK / 32);
         const int64_t kwb = kw0 + 4 * part4;
         if (vec_nk) {
-          R.b[it] = ld128(rb, rb3, kwb < KW ? b_off[it] : OOB, b_w3[it]);
+          R.b[it] = ld128(rb, rb3, kwb < KW ? b_off[it] : OOB, b_w3[it], it);
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) R.b[it][j] = ld32(rb, rb3, kwb + j < KW ? b_off[it] + 4 * j : OOB, b_w3[it]);
+          for (int j = 0; j < 4; ++j) R.b[it][j] = ld32(rb, rb3, kwb + j < KW ? b_off[it] + 4 * j : OOB, b_w3[it], it);
         }
       }
     }
-#pragma unroll
-    for (int j = 0; j < WN; ++j)
-#pragma unroll
-      for (int t = 0; t < TILE_BLOCKS; ++t)
-        sc[j][t] = biq::bitcast<float>(__builtin_amdgcn_raw_buffer_load_b32(
-            GLU && j == 1 ? rs3 : rs, scale_off(kt / BLK + t, j), 0, 0));
   };
 
   // ---- registers -> LDS buffer (activation conversion to f16 slot order happens here)
-  auto store_tile = [&](const TileRegs<G, XMODE> &R, int buf) {
+  auto store_tile = [&](const TileRegs<G, XMODE, TILE_BLOCKS> &R, int buf) {
 #pragma unroll
     for (int it = 0; it < G::A_CHUNKS; ++it) {
       const int c = tid + it * NT;
@@ -417,8 +455,10 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     for (int it = 0; it < G::B_CHUNKS; ++it) {
       const int c = tid + it * NT;
       if constexpr (LAYOUT == BIQ_Q4_KN_AXIS1) {
-        const int kwr = c / (BN / 4), nc = (c % (BN / 4)) * 4;
-        *reinterpret_cast<u32x4_t *>(&Bs[buf][kwr * B_LD + nc]) = R.b[it];
+        int kwr, nc;
+        bool w3;
+        kn_group(it, kwr, nc, w3);
+        *reinterpret_cast<u32x4_t *>(&Bs[buf][kwr * B_LD + nc + (w3 ? BNO : 0)]) = R.b[it];
       } else {
         const int nl = c / (BK / 32), part4 = c % (BK / 32);
 #pragma unroll
@@ -446,25 +486,44 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
       w[j] = Bs[buf][(2 * s + lh) * B_LD + (GLU ? j * BNO + wn * 32 : wn * (32 * WN) + 32 * j) + l32];
   };
 
-  // Pipeline: R holds tile t+1 while tile t computes; tile t+1 is stored into the other LDS
-  // buffer at the start of iteration t (its conversion overlaps the first LDS reads of tile t)
-  // and the loads of tile t+2 are issued right after, a whole tile ahead of their use.
-  TileRegs<G, XMODE> R;
-  float sc[WN][TILE_BLOCKS], sc_next[WN][TILE_BLOCKS];
-  load_tile(k_lo, R, sc);
-  store_tile(R, 0);
-  load_tile(k_lo + BK, R, sc_next);
+  // Pipeline, PF register sets deep: while tile t computes from one LDS buffer, register set
+  // t % PF holds tile t+1 (stored into the other LDS buffer at the start of iteration t, its
+  // conversion overlapping the first LDS reads of tile t) and is then refilled with tile t+1+PF,
+  // so every global load has PF whole tiles to arrive.  Iterations go in pairs so that every set is named at compile time: a loaded
+  // register is never copied while its load is in flight (a copy would make the wave wait for
+  // it).  Two sets where the registers allow it without spilling in the loop, else one.  The
+  // block scales travel in the same sets.
+  constexpr int PF = PF_SETS<LAYOUT, XMODE, BLK>;
+  constexpr int NTT = (PF == 2 || TPB == 2) ? 2 : 1;  // K tiles per loop iteration
+  TileRegs<G, XMODE, TILE_BLOCKS> RS[PF];
+  float sc_hold[WN][TILE_BLOCKS];  // scales of the tile computed next, copied out of its set
+  load_tile(k_lo, RS[0]);
+  store_tile(RS[0], 0);
+#pragma unroll
+  for (int j = 0; j < WN; ++j)
+#pragma unroll
+    for (int t = 0; t < TILE_BLOCKS; ++t) sc_hold[j][t] = RS[0].sc[j][t];
+  // issued in set order, as the loop issues them (the wave's wait counts assume it)
+#pragma unroll
+  for (int p = 0; p < PF; ++p) {
+    load_tile(k_lo + (1 + p) * BK, RS[p]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   __syncthreads();
 
   int buf = 0;
-  // Outer iterations cover whole quantisation blocks (or one K tile of several small blocks),
-  // so the first / last step of every block is known at compile time: the MFMA chain of a block
-  // starts from an inline zero and no accumulator is copied or selected at run time.
-  for (int64_t kg = k_lo; kg < k_hi; kg += UNIT) {
+  // A pair of iterations covers whole quantisation blocks (TPB is 1 or 2), so the first / last
+  // step of every block is known at compile time: the MFMA chain of a block starts from an inline
+  // zero and no accumulator is copied or selected at run time.  With two register sets a segment
+  // with an odd number of tiles (TPB 1) ends at K, and the second tile of its last pair lies
+  // wholly past K: its
+  // loads read zeros (activations, words and scales), so it adds exact zeros.  (Skipping it
+  // would put a join in the loop, where the compiler waits for the whole prefetch.)
+  for (int64_t kg = k_lo; kg < k_hi; kg += NTT * BK) {
 #pragma unroll
-    for (int tt = 0; tt < TPB; ++tt) {
+    for (int tt = 0; tt < NTT; ++tt) {
       const int64_t kt = kg + tt * BK;
-      const bool has_next = kt + BK < K;
+      TileRegs<G, XMODE, TILE_BLOCKS> &R = RS[tt % PF];
 
       half8_t a_cur[WM][NSPLIT], a_nxt[WM][NSPLIT];
       uint32_t w_cur[WN], w_nxt[WN];
@@ -474,17 +533,18 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
 #pragma unroll
       for (int j = 0; j < WN; ++j)
 #pragma unroll
-        for (int t = 0; t < TILE_BLOCKS; ++t) sc_cur[j][t] = sc[j][t];
+        for (int t = 0; t < TILE_BLOCKS; ++t) sc_cur[j][t] = sc_hold[j][t];
       // Staging and prefetch run unconditionally: past the end of K the buffer loads return
-      // zeros and the last tile's store lands in a buffer nobody reads again.  (A branch here
-      // makes the compiler merge the freshly loaded registers at the join, which waits for the
-      // whole prefetch before the first MFMA.)
+      // zeros and a store past the last tile lands in a buffer nobody reads again.  (A branch
+      // here makes the compiler merge the freshly loaded registers at the join, which waits for
+      // the whole prefetch before the first MFMA.)  The set's scales are copied out after the
+      // store, which has waited for the set anyway.
       store_tile(R, buf ^ 1);
 #pragma unroll
       for (int j = 0; j < WN; ++j)
 #pragma unroll
-        for (int t = 0; t < TILE_BLOCKS; ++t) sc[j][t] = sc_next[j][t];
-      load_tile(kt + 2 * BK, R, sc_next);
+        for (int t = 0; t < TILE_BLOCKS; ++t) sc_hold[j][t] = R.sc[j][t];
+      load_tile(kt + (1 + PF) * BK, R);
 #pragma unroll
       for (int j = 0; j < WN; ++j) b_cur[j] = unpack_q4_f16(w_cur[j]);
 
@@ -513,8 +573,8 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
           }
         } else {
           constexpr int SPB = BLK / 16;  // K16 steps per block
-          const bool first = BLK >= BK ? (tt == 0 && s == 0) : (s % SPB) == 0;
-          const bool last = BLK >= BK ? (tt == TPB - 1 && s == BK / 16 - 1) : (s % SPB) == SPB - 1;
+          const bool first = BLK >= BK ? (tt % TPB == 0 && s == 0) : (s % SPB) == 0;
+          const bool last = BLK >= BK ? (tt % TPB == TPB - 1 && s == BK / 16 - 1) : (s % SPB) == SPB - 1;
           const int tb = BLK >= BK ? 0 : s / SPB;
 #pragma unroll
           for (int i = 0; i < WM; ++i)
@@ -581,7 +641,7 @@ struct Q4Args {
 // parts of a tile plus the cost of writing and reading back a round of partials (~0.13 tile),
 // plus the tail reduction's read of a tile's partials (~0.012 tile per part).  A tail that is
 // already most of a round stays whole.
-SkPlan plan_tail(int64_t T, int64_t units, int cus) {
+SkPlan plan_tail(int64_t T, int64_t units, int64_t granule, int cus) {
   SkPlan p{(int)T, 0, 1, units, nullptr};
   const char *env = getenv("BIQ_GEMM_STREAMK");
   if (cus <= 0 || units < 2 || (env && env[0] == '0')) return p;
@@ -589,7 +649,7 @@ SkPlan plan_tail(int64_t T, int64_t units, int cus) {
   if (tail == 0) return p;
   double best = 1.0;
   int parts = 1;
-  for (int s = 2; s <= 16 && s <= units; ++s) {
+  for (int s = 2; s <= 16 && s <= units / granule; ++s) {
     const int64_t rounds = (tail * s + cus - 1) / cus;
     const double est = rounds * (1.0 / s + 0.13) + 0.012 * s;
     if (est < best - 0.05) {
@@ -611,7 +671,8 @@ int launch_geo(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const
   constexpr int64_t UNIT = (int64_t)(B >= GG::BK ? B : GG::BK);
   const int tiles_m = (int)((M + GG::BM - 1) / GG::BM), tiles_n = (int)((N + BNO - 1) / BNO);
   const int64_t T = (int64_t)tiles_m * tiles_n;
-  SkPlan plan = plan_tail(T, (K + UNIT - 1) / UNIT, biq::device_cu_count());
+  SkPlan plan = plan_tail(T, (K + UNIT - 1) / UNIT, PART_GRANULE<LAYOUT, XMODE, B, GG::BK>,
+                         biq::device_cu_count());
   const int tail = (int)(T - plan.dp_tiles);
   if (plan.sk_wgs > 0) {
     void *part = nullptr;
