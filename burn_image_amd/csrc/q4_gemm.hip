@@ -169,14 +169,14 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int tiles_m, int tiles_
   tile_n = (pid % in_group) / gsize;
 }
 
-// Epilogue of one wave's accumulators, registers r in [r_lo, r_hi) of each 32 x 32 tile: bias
-// (or the SwiGLU gate), conversion, store.  Register r of MFMA tile (i, j) holds row
-// 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4 and column 32 j + lane % 32 of the wave tile.
+// Epilogue of one wave's accumulators: bias (or the SwiGLU gate), conversion, store.  Register r
+// of MFMA tile (i, j) holds row 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4 and column
+// 32 j + lane % 32 of the wave tile.
 template <class G, bool GLU>
 __device__ __forceinline__ void store_tile_out(const floatx16_t (&acc)[G::WM][G::WN], int64_t m0,
                                                int64_t n0, const float *__restrict__ bias,
                                                void *__restrict__ yv, int y_dtype, int64_t M,
-                                               int64_t N, int r_lo, int r_hi) {
+                                               int64_t N) {
   constexpr int WM = G::WM, WN = G::WN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
@@ -190,7 +190,6 @@ __device__ __forceinline__ void store_tile_out(const floatx16_t (&acc)[G::WM][G:
     for (int i = 0; i < WM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        if (r < r_lo || r >= r_hi) continue;
         const int64_t row = m0 + wm * (32 * WM) + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (row >= M) continue;
         float v = acc[i][j][r] + bv;
@@ -209,43 +208,56 @@ __device__ __forceinline__ void store_tile_out(const floatx16_t (&acc)[G::WM][G:
   }
 }
 
-// Tail reduction: workgroup (tile t, register group g) adds the `parts` partials of tail tile t
-// in K order for registers [4 g, 4 g + 4) of every MFMA tile and writes those outputs.
+// Tail reduction.  One thread takes one output register q of four consecutive source threads
+// of one tail tile (one 16-byte load per part, coalesced), adds the `parts` partials in K order
+// and writes the four outputs: same rows and columns, bias and SwiGLU gate as the GEMM epilogue
+// (store_tile_out) would have used for those registers.
+constexpr int RED_THREADS = 256;
 template <class G, bool GLU>
-__global__ void __launch_bounds__(G::NTHREADS)
+__global__ void __launch_bounds__(RED_THREADS)
     q4_tail_reduce_kernel(const float *__restrict__ part, int tail, int parts, int dp_tiles,
                           int tiles_m, int tiles_n, const float *__restrict__ bias,
                           void *__restrict__ yv, int y_dtype, int64_t M, int64_t N) {
-  constexpr int WM = G::WM, WN = G::WN, NT = G::NTHREADS, PART = G::BM * G::BN, RG = 4;
+  constexpr int WM = G::WM, WN = G::WN, NT = G::NTHREADS, PART = G::BM * G::BN;
   constexpr int BNO = GLU ? G::BN / 2 : G::BN;
-  const int64_t t = blockIdx.x / (16 / RG);
-  const int r_lo = (int)(blockIdx.x % (16 / RG)) * RG;
-  const int tid = threadIdx.x;
+  constexpr int QN = GLU ? WM * 16 : WM * WN * 16;  // output registers per source thread
+  const int64_t per_tile = (int64_t)QN * (NT / 4);
+  const int64_t gid = (int64_t)blockIdx.x * RED_THREADS + threadIdx.x;
+  const int64_t t = gid / per_tile;
+  if (t >= tail) return;
+  const int rem = (int)(gid % per_tile);
+  const int qo = rem / (NT / 4), ts = (rem % (NT / 4)) * 4;
+  const int i = GLU ? qo / 16 : qo / (WN * 16), j = GLU ? 0 : (qo / 16) % WN, r = qo % 16;
+  const int q = (i * WN + j) * 16 + r;  // GLU: W3's register of the same output is q + 16
+  floatx4_t a = {0.0f, 0.0f, 0.0f, 0.0f}, g = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+  for (int p = 0; p < parts; ++p) {
+    const float *src = part + ((int64_t)p * tail + t) * PART + ts;
+    a += *reinterpret_cast<const floatx4_t *>(src + q * NT);
+    if constexpr (GLU) g += *reinterpret_cast<const floatx4_t *>(src + (q + 16) * NT);
+  }
   int64_t tile_m, tile_n;
   tile_coords(dp_tiles + t, tiles_m, tiles_n, tile_m, tile_n);
-  floatx16_t acc[WM][WN];
+  const int64_t m0 = tile_m * G::BM, n0 = tile_n * BNO;
 #pragma unroll
-  for (int i = 0; i < WM; ++i)
-#pragma unroll
-    for (int j = 0; j < WN; ++j) acc[i][j] = biq::zero16();
-  for (int p = 0; p < parts; ++p) {
-    const float *src = part + ((int64_t)p * tail + t) * PART;
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-      for (int j = 0; j < WN; ++j)
-#pragma unroll
-        for (int r = 0; r < RG; ++r)
-          acc[i][j][r_lo + r] += src[((i * WN + j) * 16 + r_lo + r) * NT + tid];
+  for (int e = 0; e < 4; ++e) {
+    const int st = ts + e, lane = st & 63, wave = st >> 6;
+    const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N, l32 = lane & 31, lh = lane >> 5;
+    const int64_t row = m0 + wm * (32 * WM) + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+    const int64_t col = GLU ? n0 + wn * 32 + l32 : n0 + wn * (32 * WN) + 32 * j + l32;
+    if (row >= M || col >= N) continue;
+    float v = a[e] + ((!GLU && bias) ? bias[col] : 0.0f);
+    if constexpr (GLU) v = v / (1.0f + __expf(-v)) * g[e];
+    if (y_dtype == BIQ_DTYPE_F32) {
+      reinterpret_cast<float *>(yv)[row * N + col] = v;
+    } else if (y_dtype == BIQ_DTYPE_F16) {
+      reinterpret_cast<_Float16 *>(yv)[row * N + col] = (_Float16)v;
+    } else {
+      reinterpret_cast<uint16_t *>(yv)[row * N + col] = (uint16_t)biq::f32_to_bf16_bits(v);
+    }
   }
-  store_tile_out<G, GLU>(acc, tile_m * G::BM, tile_n * BNO, bias, yv, y_dtype, M, N, r_lo, r_lo + RG);
 }
 
-// GLU: the SwiGLU form y = silu(x . W1) * (x . W3) of the reference's feed-forward
-// (crates/burn_boogu/src/model/feed_forward.rs:32-36).  A workgroup then covers BN / 2 output
-// columns of both weights: the word tile holds W1's columns in its first half and W3's in its
-// second, so a wave's two 32-column MFMA tiles are W1 and W3 for the SAME output columns and the
-// epilogue combines them in registers.
 template <class G, int LAYOUT, int XMODE, int BLK, bool GLU>
 __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     q4_gemm_kernel(const void *__restrict__ xv, int64_t ldx, const uint32_t *__restrict__ words,
@@ -609,7 +621,7 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
 
   // ---------------- epilogue: bias (or the SwiGLU gate), convert, store ---------------------
   if (ku0 == 0 && ku1 == units) {  // the whole K of the tile
-    store_tile_out<G, GLU>(acc, m0, n0, bias, yv, y_dtype, M, N, 0, 16);
+    store_tile_out<G, GLU>(acc, m0, n0, bias, yv, y_dtype, M, N);
     continue;
   }
   // ---- tail chunk: the partial goes to slot c, register-major (element (register q, thread
@@ -688,7 +700,10 @@ int launch_geo(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const
   if (plan.sk_wgs > 0) {
     const int st = biq::check_launch(GLU ? "q4 linear swiglu" : "q4 linear");
     if (st != BIQ_OK) return st;
-    hipLaunchKernelGGL((q4_tail_reduce_kernel<GG, GLU>), dim3((unsigned)tail * 4), dim3(GG::NTHREADS),
+    constexpr int QN = GLU ? GG::WM * 16 : GG::WM * GG::WN * 16;
+    const int64_t threads = (int64_t)tail * QN * (GG::NTHREADS / 4);
+    hipLaunchKernelGGL((q4_tail_reduce_kernel<GG, GLU>),
+                       dim3((unsigned)((threads + RED_THREADS - 1) / RED_THREADS)), dim3(RED_THREADS),
                        0, s, plan.part, tail, plan.parts, plan.dp_tiles, tiles_m, tiles_n, bias, y,
                        y_dtype, M, N);
   }
