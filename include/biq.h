@@ -88,7 +88,11 @@ int biq_q4_dequant_f32(void *stream, const uint32_t *words, const float *scales,
  * {F32, F16, BF16}; bias may be NULL.  Requirements: K % 8 == 0, K % block == 0, N % 8 == 0,
  * block in {8, 16, 32, 64, 128}.  Arithmetic: the signed nibbles are exact in f16, activations
  * enter the matrix cores as f16 (f32 inputs as an exact-to-2^-22 f16 hi+lo pair), products
- * accumulate in f32 per K-block, and each block sum is scaled by its f32 scale in f32. */
+ * accumulate in f32 per K-block, and each block sum is scaled by its f32 scale in f32.
+ * Scratch: calls with M <= 16 and an f32 output, and calls whose last tiles are split along K,
+ * use the library's grow-only scratch for (device, stream); it can only grow outside stream
+ * capture (BIQ_ERR_UNSUPPORTED there: make the same call once before capturing).  Results are
+ * deterministic; rows of a K-split tile are summed in another order than rows of a whole tile. */
 int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   const uint32_t *words, const float *scales, int layout, int block, int64_t N,
                   const float *bias, void *y, int y_dtype);
