@@ -136,6 +136,10 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
     else
       qf[s] = u32x4_t{0u, 0u, 0u, 0u};
   }
+  // Q is in registers before the K/V pipeline starts: otherwise the loop's first MFMA, reached
+  // from here with Q's loads in flight and from the back-edge with a K/V set in flight, makes
+  // the compiler wait for every outstanding load at the top of each iteration.
+  __builtin_amdgcn_s_waitcnt(0);
 
   // ---- key range of this workgroup and visibility bounds of this lane's query
   int64_t kv_begin = 0, kv_end = p.Skv;
@@ -261,20 +265,35 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
   // when a new score exceeds it by more than 2^8, so most tiles skip the O rescale.
   float m_run = -INFINITY, l_run = 0.0f;
 
-  KVRegs<DP, InT> R;
+  // Two register sets (16-bit inputs): while tile t computes, set t % 2 receives tile t+2 and set (t+1) % 2
+  // (loaded one tile earlier) is stored into the other LDS buffer at the end, so every load has
+  // two tiles of compute to land.  Iterations go in pairs so both sets are named at compile time
+  // (a copy of a register whose load is still in flight would make the wave wait for it).  An
+  // odd tile count runs one more tile past the key range: every key of it is masked (outside
+  // every lane's visible range), so it adds exact zeros -- skipping it instead would put a join
+  // in the loop, where the compiler waits for the whole prefetch.
+  // f32 inputs are narrowed to f16 as they load (which waits for them), and a second set would
+  // not fit their registers: one set there.
+  constexpr int NS = F32IN ? 1 : 2;
+  KVRegs<DP, InT> RS[NS];
   int buf = 0;
   if (kv_begin < kv_end) {
-    load_tile(kv_begin, R);
-    store_tile(R, 0);
+    load_tile(kv_begin, RS[0]);
+    store_tile(RS[0], 0);
+#pragma unroll
+    for (int p1 = 1; p1 < NS; ++p1) load_tile(kv_begin + p1 * BKV, RS[p1]);
   }
   __syncthreads();
 
-  for (int64_t kv0 = kv_begin; kv0 < kv_end; kv0 += BKV, buf ^= 1) {
-    // The next tile's loads and LDS stores run unconditionally: past the key range the buffer
-    // loads return zeros and the last store lands in a buffer nobody reads again.  (A branch
-    // here makes the compiler merge the prefetched registers at the join, which waits for the
-    // whole prefetch before the first MFMA.)
-    load_tile(kv0 + BKV, R);
+  for (int64_t kv00 = kv_begin; kv00 < kv_end; kv00 += NS * BKV) {
+#pragma unroll
+  for (int tt = 0; tt < NS; ++tt, buf ^= 1) {
+    const int64_t kv0 = kv00 + tt * BKV;
+    // The loads and LDS stores run unconditionally: past the key range the buffer loads return
+    // zeros and a store lands in a buffer nobody reads again.  (A branch here makes the compiler
+    // merge the prefetched registers at the join, which waits for the whole prefetch before the
+    // first MFMA.)
+    load_tile(kv0 + NS * BKV, RS[tt]);
 
     // ---- S^T = K Q^T for the tile's 64 keys (2 x 32)
     floatx16_t sacc[2];
@@ -363,8 +382,9 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
       }
     }
 
-    store_tile(R, buf ^ 1);
+    store_tile(RS[(tt + 1) % NS], buf ^ 1);
     __syncthreads();
+  }
   }
 
   // ---- normalise and store O[b, h, qi, d]
