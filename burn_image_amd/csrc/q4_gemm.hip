@@ -67,13 +67,14 @@ __device__ __forceinline__ u32x4_t bf16x8_to_f16_slots(u32x4_t v) {
   return r;
 }
 
-// 8 f16 -> slot order [0,4,1,5,2,6,3,7].
+// 8 f16 -> slot order [0,4,1,5,2,6,3,7]: one byte permute per output word (v_perm_b32 picks
+// bytes 0-3 from its second operand and 4-7 from its first).
 __device__ __forceinline__ u32x4_t f16x8_to_slots(u32x4_t v) {
   u32x4_t r;
-  r[0] = (v[0] & 0xffffu) | (v[2] << 16);
-  r[1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
-  r[2] = (v[1] & 0xffffu) | (v[3] << 16);
-  r[3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
+  r[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);  // (v0.lo, v2.lo)
+  r[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);  // (v0.hi, v2.hi)
+  r[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+  r[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
   return r;
 }
 
