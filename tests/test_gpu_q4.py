@@ -108,6 +108,27 @@ def test_gpu_q4_linear_blocks_dtypes_tails(gpu, oracle, layout, block, xdt):
     assert_parity(y, ref, f"blk{block}_l{layout}_{xdt}")
 
 
+@pytest.mark.parametrize("K", [128, 384, 1152])
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
+@pytest.mark.parametrize("glu", [False, True])
+def test_gpu_q4_linear_odd_tile_counts(gpu, oracle, K, xdt, glu):
+    """The [K/8, N] block-128 path streams K tiles in pairs: an odd tile count (1, 3, 9 tiles of
+    128) runs one extra tile past K whose loads read zeros, with and without the tail split."""
+    M, N = 150, 520
+    x = W.activations(21, K, M, K, xdt)
+    w1, s1 = W.q4_weight(21, K + 1, K, N, layout=1)
+    q1 = weight(w1, s1, 1, 128, K, N, gpu)
+    xd = dev(x, TORCH_DT[xdt], gpu)
+    ref = oracle.q4_linear_f64(x, w1, s1, 1, 128, N)
+    if glu:
+        w3, s3 = W.q4_weight(21, K + 2, K, N, layout=1)
+        y = host(B.q_matmul_swiglu(xd, q1, weight(w3, s3, 1, 128, K, N, gpu)))
+        ref = silu_gate_ref(ref, oracle.q4_linear_f64(x, w3, s3, 1, 128, N))
+    else:
+        y = host(B.q_matmul(xd, q1))
+    assert_parity(y, ref.astype(np.float32), f"odd_tiles_K{K}_{xdt}_glu{int(glu)}")
+
+
 def test_gpu_q4_linear_bias_and_output_dtypes(gpu, oracle):
     M, K, N = 130, 256, 136
     x = W.activations(13, 1, M, K, "bf16")
