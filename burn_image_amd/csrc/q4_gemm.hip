@@ -19,12 +19,13 @@
 //
 // Schedule: 512 threads = 8 waves (2 per SIMD) in a 2 (M) x 4 (N) grid; workgroup tile
 // 128 x 256, wave tile 64 x 64 (2 x 2 MFMA 32 x 32 tiles); K advances 128 per tile (64 for f32
-// activations).  While the
-// waves run the MFMAs of tile t from one LDS buffer, every thread already holds tile t+1's global
-// loads (activations, packed words and block scales) in registers; it converts and stores them
-// into the other LDS buffer afterwards, so one barrier per tile separates the two.  Workgroups are
-// numbered so that each XCD (hardware places workgroup i on XCD i % 8) walks a compact,
-// M-grouped block of output tiles, keeping the shared activation and weight tiles in its L2.
+// activations and blocks <= 16).  While the waves run the MFMAs of tile t from one LDS buffer,
+// the threads hold the global loads (activations, packed words, block scales) of the next one or
+// two tiles in registers; tile t+1 is converted and stored into the other LDS buffer during
+// tile t, so one barrier per tile separates the two.  Workgroups are numbered so that each XCD
+// (hardware places workgroup i on XCD i % 8) walks a compact, M-grouped block of output tiles,
+// keeping the shared activation and weight tiles in its L2.  When the tiles leave the last
+// round of workgroups mostly idle, the tail tiles are split along K (SkPlan below).
 #include <stdlib.h>
 
 #include "common.h"
