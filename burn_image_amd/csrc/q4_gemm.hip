@@ -655,15 +655,22 @@ struct Q4Args {
 // parts of a tile plus the cost of writing and reading back a round of partials (~0.13 tile),
 // plus the tail reduction's read of a tile's partials (~0.012 tile per part).  A tail that is
 // already most of a round stays whole.
+// BIQ_GEMM_STREAMK in the environment: "0" (or "1") keeps every tile whole; a number n > 1
+// forces n parts (capped to what K allows) -- a tuning switch.  Measured against the model's
+// choice: 1024x4096x4096 (128 tiles) 79.5 -> 57.2 us with 2 parts (chosen); 1024x4096x6144 (192
+// tiles) and the 4608-row O / MLP shapes are fastest whole (chosen); 4608x3072x9216: 6 parts
+// (chosen) 403 us, 8 parts 400 us, whole 423 us.
 SkPlan plan_tail(int64_t T, int64_t units, int64_t granule, int cus) {
   SkPlan p{(int)T, 0, 1, units, nullptr};
   const char *env = getenv("BIQ_GEMM_STREAMK");
-  if (cus <= 0 || units < 2 || (env && env[0] == '0')) return p;
+  const int forced = env ? atoi(env) : -1;
+  if (cus <= 0 || units < 2 || forced == 0 || forced == 1) return p;
   const int64_t tail = T % cus;
   if (tail == 0) return p;
+  const int64_t max_parts = units / granule < 16 ? units / granule : 16;
   double best = 1.0;
   int parts = 1;
-  for (int s = 2; s <= 16 && s <= units / granule; ++s) {
+  for (int s = 2; s <= max_parts; ++s) {
     const int64_t rounds = (tail * s + cus - 1) / cus;
     const double est = rounds * (1.0 / s + 0.13) + 0.012 * s;
     if (est < best - 0.05) {
@@ -671,7 +678,8 @@ SkPlan plan_tail(int64_t T, int64_t units, int64_t granule, int cus) {
       parts = s;
     }
   }
-  if (parts == 1) return p;
+  if (forced > 1) parts = forced < max_parts ? forced : (int)max_parts;
+  if (parts <= 1) return p;
   p.dp_tiles = (int)(T - tail);
   p.parts = parts;
   p.sk_wgs = (int)(tail * parts < cus ? tail * parts : cus);
