@@ -8,7 +8,7 @@ Two independent statements of the reference algorithms live here:
 * ``np_*``: vectorised numpy restatements used to cross-check the C oracle on small inputs.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import this
-module, and only as the checker; the product library never calls it.  Reference citations are
+module, and only to check results against; the product library never calls it.  Reference citations are
 ``file:line`` relative to the reference repository root.
 """
 from __future__ import annotations
