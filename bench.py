@@ -60,16 +60,17 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-rows", type=int, default=1152,
-                    help="query rows / activation rows of the bounded CPU sample")
+    ap.add_argument("--cpu-rows", type=int, default=4608,
+                    help="query rows / activation rows of the CPU sample (4608 = the whole step)")
     return ap.parse_args()
 
 
 def cpu_baseline(args, words_np, scales_np, x_np, q_np, k_np, v_np):
-    """Restated Burn NdArray CPU path on a bounded sample of the same workload: the four Q4
-    GEMMs over the first `cpu_rows` activation rows (dequantise + f32 matmul) and the joint
-    attention over the first `cpu_rows` query rows of every head (query-chunked f32 softmax).
-    Each op's rate is measured; the full step's CPU time is extrapolated op by op."""
+    """Restated Burn NdArray CPU path on the same workload: the four Q4 GEMMs over the first
+    `cpu_rows` activation rows (dequantise + f32 matmul) and the joint attention over the first
+    `cpu_rows` query rows of every head (query-chunked f32 softmax).  By default `cpu_rows` is
+    all 4608 rows, so one whole step is timed (a few seconds on 16 host threads); a smaller
+    sample times each op on its rows and extrapolates the step op by op."""
     from oracle import oracle as O
     O.build()
     rows = args.cpu_rows
@@ -91,15 +92,19 @@ def cpu_baseline(args, words_np, scales_np, x_np, q_np, k_np, v_np):
     detail["attention"] = rate / 1e12
     t_total += attn_flops(**ATTN) / rate
     step_flops = sum(gemm_flops(M_TOKENS, K, N) for _, K, N in GEMMS) + attn_flops(**ATTN)
+    if rows >= M_TOKENS:
+        scope = ("the whole step: all 4608 rows of each Q4 GEMM and all 4608 query rows x 24 heads "
+                 "of the attention, each op timed once")
+    else:
+        scope = (f"the first {rows} of 4608 rows of each Q4 GEMM and {rows} query rows x 24 heads "
+                 f"of the attention; per-op rates extrapolated to one full step")
     return {
         "value": step_flops / t_total / 1e12,
         "unit": "TFLOP/s",
         "cores": int(threads),
         "kind": "port",
-        "sample": (f"restated Burn NdArray CPU path (dequantise + f32 matmul; query-chunked f32 "
-                   f"attention, chunk policy of attention.rs:36-45) on the first {rows} of 4608 "
-                   f"rows of each Q4 GEMM and {rows} query rows x 24 heads of the attention; "
-                   f"per-op rates extrapolated to one full step"),
+        "sample": ("restated Burn NdArray CPU path (dequantise + f32 matmul; query-chunked f32 "
+                   "attention, chunk policy of attention.rs:36-45) on " + scope),
         "per_op_tflops": {k: round(v, 5) for k, v in detail.items()},
         "ms_per_step": t_total * 1e3,
     }
