@@ -52,6 +52,7 @@ def test_storage_contract_matches_reference():
     # biq_attention: GQA heads not divisible (native_flash.rs:2828-2841 fails closed)
     (dict(Hq=4, Hkv=3), b"divisible"),
     (dict(Sq=0), b"non-empty"),
+    (dict(Skv=0), b"non-empty"),
     (dict(D=136), b"head width"),
     (dict(causal=1, Skv=7), b"Sq == Skv"),
 ])
@@ -79,3 +80,9 @@ def test_q4_linear_validation_fails_closed():
     assert lib.biq_q4_linear(None, d, 0, 4, 96, 96, d, d, 1, 64, 8, None, d, 0) == _lib.ERR_INVALID_ARG
     # N not divisible by 8
     assert lib.biq_q4_linear(None, d, 0, 4, 128, 128, d, d, 1, 128, 12, None, d, 0) == _lib.ERR_INVALID_ARG
+    # empty M, K or N fails closed with a message, on the small-M route and the GEMM route alike
+    for m, k, n in ((0, 128, 8), (0, 128, 4096), (4, 0, 8), (64, 128, 0)):
+        for y_dtype in (_lib.DTYPE_F32, _lib.DTYPE_BF16):
+            assert lib.biq_q4_linear(None, d, _lib.DTYPE_BF16, m, k, max(k, 1), d, d, 1, 128, n, None,
+                                     d, y_dtype) == _lib.ERR_INVALID_ARG
+            assert b"non-empty" in lib.biq_last_error()
