@@ -25,12 +25,17 @@
 
 namespace {
 
-constexpr int BQ = 128;      // query rows per workgroup (4 waves x 32)
 constexpr int BKV = 64;      // keys per LDS tile
-constexpr int NTHREADS = 256;
 constexpr int VT_LD = BKV + 8;  // halves per row of the transposed V tile
 
 enum MaskMode { MASK_NONE = 0, MASK_CAUSAL = 1, MASK_SEGMENT = 2, MASK_CAUSAL_SEGMENT = 3 };
+
+// Waves per workgroup (each wave owns 32 query rows; two waves per SIMD either way).  Without a
+// mask 8 waves (256 query rows) share each staged K/V tile, so a tile is loaded and written to
+// LDS once for twice the queries of a 4-wave block (measured 7-10% faster at 4608 and 18944
+// tokens).  Masked forms keep 4 waves (128 rows): a taller block widens the band of keys that
+// only some of its rows see, and the causal form measured 5% slower with 8.
+constexpr int wg_waves(int mask) { return mask == MASK_NONE ? 8 : 4; }
 
 struct AttnArgs {
   const void *q, *k, *v;
@@ -76,9 +81,9 @@ __device__ __forceinline__ int64_t segment_of(const int32_t *cu, int64_t nseg, i
 }
 
 // Per-thread register copy of one K/V tile (prefetched while the previous tile computes).
-template <int DP, typename InT>
+template <int DP, typename InT, int NT>
 struct KVRegs {
-  static constexpr int K_CHUNKS = (BKV * DP / 8) / NTHREADS;  // 8-element K groups per thread
+  static constexpr int K_CHUNKS = (BKV * DP / 8) / NT;  // 8-element K groups per thread
   static constexpr int V_GROUPS = (BKV / 4) * (DP / 8);       // 4-key x 8-dim V blocks per tile
   u32x4_t k16[K_CHUNKS];  // compute-type bits (f32 inputs are narrowed to f16 at load)
   u32x4_t v16[4];         // input bits (bf16 / f16; f32 inputs narrowed to f16 at load)
@@ -93,12 +98,14 @@ __device__ __forceinline__ u32x4_t load8_f32_as_f16(const float *p) {
 }
 
 template <int DP, typename InT, int MASK>
-__global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
+__global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_fwd_kernel(AttnArgs p) {
+  constexpr int NT = 64 * wg_waves(MASK);  // threads per workgroup
+  constexpr int BQ = 32 * wg_waves(MASK);  // query rows per workgroup
   constexpr bool BF16 = std::is_same<InT, bf16_t>::value;
   constexpr bool F32IN = sizeof(InT) == 4;
   constexpr int KS_LD = DP + 8;  // halves per row of the K tile
-  constexpr int K_CHUNKS = KVRegs<DP, InT>::K_CHUNKS;
-  constexpr int V_GROUPS = KVRegs<DP, InT>::V_GROUPS;
+  constexpr int K_CHUNKS = KVRegs<DP, InT, NT>::K_CHUNKS;
+  constexpr int V_GROUPS = KVRegs<DP, InT, NT>::V_GROUPS;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BKV * KS_LD];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[2][DP * VT_LD];
 
@@ -183,7 +190,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
   uint32_t koff[K_CHUNKS], voff[4];
 #pragma unroll
   for (int it = 0; it < K_CHUNKS; ++it) {
-    const int c = tid + it * NTHREADS;
+    const int c = tid + it * NT;
     const int row = c / (DP / 8), d0 = 8 * (c % (DP / 8));
     koff[it] = d0 < D ? (uint32_t)(row * krow_b + d0 * ESZ) : OOB;
   }
@@ -214,7 +221,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
       return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     }
   };
-  auto load_tile = [&](int64_t kv0, KVRegs<DP, InT> &R) {
+  auto load_tile = [&](int64_t kv0, KVRegs<DP, InT, NT> &R) {
     const auto rk = rsrc(kg, kv0, krow_b);
 #pragma unroll
     for (int it = 0; it < K_CHUNKS; ++it) R.k16[it] = load16(rk, koff[it]);
@@ -226,10 +233,10 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
   };
 
   // ---- registers -> LDS buffer: K row-major in the compute type, V transposed f16
-  auto store_tile = [&](const KVRegs<DP, InT> &R, int buf) {
+  auto store_tile = [&](const KVRegs<DP, InT, NT> &R, int buf) {
 #pragma unroll
     for (int it = 0; it < K_CHUNKS; ++it) {
-      const int c = tid + it * NTHREADS;
+      const int c = tid + it * NT;
       const int row = c / (DP / 8), d0 = 8 * (c % (DP / 8));
       *reinterpret_cast<u32x4_t *>(&Ks[buf][row * KS_LD + d0]) = R.k16[it];
     }
@@ -275,7 +282,7 @@ __global__ void __launch_bounds__(NTHREADS, 2) attn_fwd_kernel(AttnArgs p) {
   // f32 inputs are narrowed to f16 as they load (which waits for them), and a second set would
   // not fit their registers: one set there.
   constexpr int NS = F32IN ? 1 : 2;
-  KVRegs<DP, InT> RS[NS];
+  KVRegs<DP, InT, NT> RS[NS];
   int buf = 0;
   if (kv_begin < kv_end) {
     load_tile(kv_begin, RS[0]);
@@ -421,17 +428,17 @@ template <int DP, typename InT>
 void launch_mask(hipStream_t s, dim3 grid, const AttnArgs &a, int mask) {
   switch (mask) {
     case MASK_NONE:
-      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_NONE>), grid, dim3(NTHREADS), 0, s, a);
+      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_NONE>), grid, dim3(64 * wg_waves(MASK_NONE)), 0, s, a);
       break;
     case MASK_CAUSAL:
-      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_CAUSAL>), grid, dim3(NTHREADS), 0, s, a);
+      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_CAUSAL>), grid, dim3(64 * wg_waves(MASK_CAUSAL)), 0, s, a);
       break;
     case MASK_SEGMENT:
-      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_SEGMENT>), grid, dim3(NTHREADS), 0, s, a);
+      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_SEGMENT>), grid, dim3(64 * wg_waves(MASK_SEGMENT)), 0, s, a);
       break;
     default:
-      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_CAUSAL_SEGMENT>), grid, dim3(NTHREADS), 0,
-                         s, a);
+      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_CAUSAL_SEGMENT>), grid,
+                         dim3(64 * wg_waves(MASK_CAUSAL_SEGMENT)), 0, s, a);
       break;
   }
 }
@@ -488,7 +495,9 @@ extern "C" int biq_attention(void *stream, const void *q, const void *k, const v
       return biq::fail(BIQ_ERR_INVALID_ARG, "attention output strides must be multiples of 16 bytes");
   if (k_strides[2] * esz * BKV >= (1LL << 31) || v_strides[2] * esz * BKV >= (1LL << 31))
     return biq::fail(BIQ_ERR_UNSUPPORTED, "attention key/value row stride too large for 32-bit tile offsets");
-  if ((Sq + BQ - 1) / BQ * Hq * B > 0x7fffffffLL)
+  const int mask = (causal ? MASK_CAUSAL : 0) | (cu_seqlens ? MASK_SEGMENT : 0);
+  const int64_t bq = 32 * wg_waves(mask);
+  if ((Sq + bq - 1) / bq * Hq * B > 0x7fffffffLL)
     return biq::fail(BIQ_ERR_UNSUPPORTED, "attention grid too large");
 
   AttnArgs a;
@@ -502,8 +511,7 @@ extern "C" int biq_attention(void *stream, const void *q, const void *k, const v
   a.out_dtype = out_dtype;
   a.cu = cu_seqlens;
   a.nseg = nseg;
-  const int mask = (causal ? MASK_CAUSAL : 0) | (cu_seqlens ? MASK_SEGMENT : 0);
-  dim3 grid((unsigned)((Sq + BQ - 1) / BQ * Hq * B));
+  dim3 grid((unsigned)((Sq + bq - 1) / bq * Hq * B));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (D <= 64) launch_dtype<64>(s, grid, a, in_dtype, mask);
   else launch_dtype<128>(s, grid, a, in_dtype, mask);
