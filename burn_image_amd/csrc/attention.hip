@@ -30,12 +30,13 @@ constexpr int VT_LD = BKV + 8;  // halves per row of the transposed V tile
 
 enum MaskMode { MASK_NONE = 0, MASK_CAUSAL = 1, MASK_SEGMENT = 2, MASK_CAUSAL_SEGMENT = 3 };
 
-// Waves per workgroup (each wave owns 32 query rows; two waves per SIMD either way).  Without a
-// mask 8 waves (256 query rows) share each staged K/V tile, so a tile is loaded and written to
-// LDS once for twice the queries of a 4-wave block (measured 7-10% faster at 4608 and 18944
-// tokens).  Masked forms keep 4 waves (128 rows): a taller block widens the band of keys that
-// only some of its rows see, and the causal form measured 5% slower with 8.
-constexpr int wg_waves(int mask) { return mask == MASK_NONE ? 8 : 4; }
+// Waves per workgroup (each wave owns 32 query rows; two waves per SIMD either way).  Non-causal
+// forms run 8 waves (256 query rows) on each staged K/V tile, so a tile is loaded and written to
+// LDS once for twice the queries of a 4-wave block (measured 7-10% faster unmasked at 4608 and
+// 18944 tokens, 6-10% with per-segment masks).  Causal forms keep 4 waves (128 rows): a taller
+// block widens the band of keys that only some of its rows see, and 8 waves measured 5% slower
+// there (12% slower when waves also skipped the tiles none of their rows see).
+constexpr int wg_waves(int mask) { return (mask & MASK_CAUSAL) ? 4 : 8; }
 
 struct AttnArgs {
   const void *q, *k, *v;
