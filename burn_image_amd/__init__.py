@@ -3,7 +3,8 @@ GEMMs and exact flash attention, as hand-written HIP kernels behind a C ABI (inc
 libbiq.so), with a host-side mirror of the reference's Burn-facing operator surface."""
 from . import _lib
 from ._lib import BiqError, InvalidArgument, Unsupported, version
-from .attention import (F16_STORAGE_F32_ACCUM, STRICT_F32, AttentionKernel,
+from .attention import (F16_STORAGE_F32_ACCUM, STRICT_F32, AttentionKernel, burn_attention,
+                        check_cu_seqlens, frame_ranges_to_cu_seqlens,
                         NativeQ4FlashAttention, RmsNorm, attention,
                         effective_portable_query_chunk_size, qk_norm_rope)
 from .block import GqaAttention, RmsNormZero, SingleStreamBlock, block_glue
@@ -18,6 +19,7 @@ Q4_NK_AXIS0 = _lib.Q4_NK_AXIS0
 
 __all__ = [
     "AttentionKernel", "NativeQ4FlashAttention", "attention", "effective_portable_query_chunk_size",
+    "burn_attention", "check_cu_seqlens", "frame_ranges_to_cu_seqlens",
     "RmsNorm", "qk_norm_rope", "STRICT_F32", "F16_STORAGE_F32_ACCUM",
     "Linear", "LuminaFeedForward", "linear_forward", "q_matmul", "q_matmul_swiglu",
     "qwen_linear_forward", "Q4Weight", "from_packed",

@@ -22,6 +22,10 @@ DTYPE_F32 = 0
 DTYPE_F16 = 1
 DTYPE_BF16 = 2
 
+KEY_MASK_VALID = 0            # nonzero byte = key may be attended (Qwen attention_mask)
+KEY_MASK_VALID_FILL_MEAN = 1  # as VALID; rows with no visible key = mean of V (Qwen -1e30 fill)
+KEY_MASK_MASKED = 2           # nonzero byte = key masked out (Burn bool mask polarity)
+
 Q4_NK_AXIS0 = 0  # Qwen PackedU32(0): weight [N, K], words [N, K/8], scales [N, K/blk]
 Q4_KN_AXIS1 = 1  # Boogu PackedU32(1): weight [K, N], words [K/8, N], scales [K/blk, N]
 
@@ -42,7 +46,13 @@ SIGNATURES = {
     "biq_q4_linear_swiglu": ([_P, _P, _I, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _I], _I),
     "biq_attention": ([_P, _P, _P, _P, _P, _I, _I, _I64, _I64, _I64, _I64, _I64, _I64,
                        ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I64),
-                       ctypes.POINTER(_I64), ctypes.c_float, _I, _P, _I64], _I),
+                       ctypes.POINTER(_I64), ctypes.c_float, _I, _P, _I64, _P, _I64, _I], _I),
+    "biq_attention_burn": ([_P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64,
+                            ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I64),
+                            ctypes.POINTER(_I64), _P, ctypes.POINTER(_I64), _P, _I, _I,
+                            ctypes.c_float, _I, ctypes.c_float], _I),
+    "biq_check_cu_seqlens": ([_P, _I64, _I64], _I),
+    "biq_frame_ranges_to_cu_seqlens": ([_P, _I64, _I64, _P], _I),
     "biq_qk_norm_rope": ([_P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64,
                           ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I64),
                           _P, _P, ctypes.c_float, ctypes.c_float, _P, _P, _I64, _I, _P, _P, _P], _I),

@@ -7,11 +7,14 @@ runs in libbiq; a missing library raises.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
 
 from . import _lib
+
+ctypes_i64 = ctypes.c_int64
 
 _DTYPE_CODE = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16,
                torch.bfloat16: _lib.DTYPE_BF16}
@@ -40,15 +43,56 @@ def _strides_bhsd(t: torch.Tensor, name: str):
     return _lib.strides3((t.stride(0), t.stride(1), t.stride(2)))
 
 
+def check_cu_seqlens(cu_seqlens, seq_len: int) -> None:
+    """Host-side validation of a segment table (libbiq's biq_check_cu_seqlens): starts at 0,
+    strictly ascending, ends at `seq_len`.  Raises InvalidArgument otherwise."""
+    import numpy as np
+    cu = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int64))
+    if cu.ndim != 1 or cu.size < 2:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "cu_seqlens must list at least one segment")
+    if cu.min() < -2**31 or cu.max() >= 2**31:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "cu_seqlens values must fit int32")
+    cu32 = cu.astype(np.int32)
+    _lib.check(_lib.load().biq_check_cu_seqlens(cu32.ctypes.data, cu32.size - 1, int(seq_len)))
+
+
+def frame_ranges_to_cu_seqlens(frame_ranges, seq_len: int):
+    """Qwen vision frame ranges [(start, end), ...] (crates/burn_qwen3_vl/src/vision.rs:319-386)
+    -> int32 segment table, validated on the host (frames tile [0, seq_len) in order)."""
+    import numpy as np
+    r = np.ascontiguousarray(np.asarray(frame_ranges, dtype=np.int64).reshape(-1, 2))
+    cu = np.zeros(r.shape[0] + 1, np.int32)
+    _lib.check(_lib.load().biq_frame_ranges_to_cu_seqlens(r.ctypes.data, r.shape[0], int(seq_len),
+                                                          cu.ctypes.data))
+    return cu
+
+
+def _device_cu(cu_seqlens, seq_len: int, device) -> torch.Tensor:
+    """A host segment table is validated and copied; a device int32 table is used as given (the
+    kernel clamps every bound it reads)."""
+    if isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.is_cuda:
+        if cu_seqlens.dtype != torch.int32:
+            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "cu_seqlens must be int32")
+        return cu_seqlens.contiguous()
+    host = cu_seqlens.cpu().numpy() if isinstance(cu_seqlens, torch.Tensor) else cu_seqlens
+    check_cu_seqlens(host, seq_len)
+    import numpy as np
+    return torch.from_numpy(np.asarray(host, dtype=np.int32)).to(device)
+
+
 def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *,
               is_causal: bool = False, scale: Optional[float] = None,
-              cu_seqlens: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+              cu_seqlens=None, key_mask: Optional[torch.Tensor] = None,
+              key_mask_mode: int = _lib.KEY_MASK_VALID, out: Optional[torch.Tensor] = None,
               out_dtype: Optional[torch.dtype] = None, stream: Optional[int] = None) -> torch.Tensor:
     """softmax(Q K^T * scale) V over [B, H, S, D] views (any batch/head/seq strides, D
     contiguous).  K/V may carry fewer heads (GQA: query head h reads h / (Hq / Hkv)).
-    ``cu_seqlens`` (int32 [nseg + 1]) adds the block-diagonal segment mask of a packed
-    sequence; ``is_causal`` masks key j > query i.  Default scale 1/sqrt(D); default output dtype
-    is the input dtype."""
+    ``cu_seqlens`` (int32 [nseg + 1]; a host table is validated first) adds the block-diagonal
+    segment mask of a packed sequence; ``is_causal`` masks key j > query i; ``key_mask``
+    ([B, Skv] bool/uint8 on the GPU) masks keys per batch, read by ``key_mask_mode``
+    (KEY_MASK_VALID: True = attend; KEY_MASK_VALID_FILL_MEAN: also rows with no visible key get
+    mean(V), Qwen's -1e30 fill; KEY_MASK_MASKED: True = masked).  Default scale 1/sqrt(D);
+    default output dtype is the input dtype."""
     for name, t in (("query", query), ("key", key), ("value", value)):
         if not t.is_cuda:
             raise ValueError(f"attention {name} must be a GPU tensor")
@@ -72,17 +116,58 @@ def attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *,
         raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention out has the wrong shape or dtype")
     cu_ptr, nseg = None, 0
     if cu_seqlens is not None:
-        if cu_seqlens.dtype != torch.int32 or not cu_seqlens.is_cuda:
-            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "cu_seqlens must be an int32 GPU tensor")
-        cu_seqlens = cu_seqlens.contiguous()
+        cu_seqlens = _device_cu(cu_seqlens, Sq, query.device)
         cu_ptr, nseg = cu_seqlens.data_ptr(), cu_seqlens.numel() - 1
+    km_ptr, km_stride = None, 0
+    if key_mask is not None:
+        if not key_mask.is_cuda or key_mask.dtype not in (torch.bool, torch.uint8, torch.int8):
+            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "key_mask must be a bool/uint8 GPU tensor")
+        if key_mask.dim() != 2 or key_mask.shape[1] != Skv or key_mask.shape[0] not in (1, B):
+            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "key_mask must be [B or 1, Skv]")
+        if key_mask.stride(1) != 1:
+            key_mask = key_mask.contiguous()
+        km_ptr = key_mask.data_ptr()
+        km_stride = key_mask.stride(0) if key_mask.shape[0] == B and B > 1 else 0
     s = torch.cuda.current_stream(query.device).cuda_stream if stream is None else stream
     _lib.check(_lib.load().biq_attention(
         s, query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(),
         _DTYPE_CODE[query.dtype], _DTYPE_CODE[odt], B, Hq, Hkv, Sq, Skv, D,
         _strides_bhsd(query, "query"), _strides_bhsd(key, "key"), _strides_bhsd(value, "value"),
         _strides_bhsd(out, "output"), float(scale) if scale else 0.0, int(bool(is_causal)),
-        cu_ptr, nseg))
+        cu_ptr, nseg, km_ptr, km_stride, int(key_mask_mode)))
+    return out
+
+
+def burn_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                   mask: Optional[torch.Tensor] = None, attn_bias: Optional[torch.Tensor] = None, *,
+                   is_causal: bool = False, scale: Optional[float] = None,
+                   softcap: Optional[float] = None, stream: Optional[int] = None) -> torch.Tensor:
+    """Burn's ModuleOps::attention (patches/burn-cubecl-0.21.0/src/ops/module.rs:342-367) on
+    libbiq: [B, H, S, D] tensors of one dtype, output in that dtype.  `mask` is a bool tensor
+    broadcastable to [B, H, Sq, Skv] with True = masked; only key-padding masks (broadcast over
+    heads and queries) run, any other mask, an attn_bias or a softcap raises Unsupported."""
+    B, Hq, Sq, D = query.shape
+    Hkv, Skv = key.shape[1], key.shape[2]
+    if not (query.dtype == key.dtype == value.dtype) or query.dtype not in _DTYPE_CODE:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention Q/K/V must share an F32/F16/BF16 dtype")
+    out = torch.empty((B, Hq, Sq, D), dtype=query.dtype, device=query.device)
+    m_ptr, m_str = None, None
+    if mask is not None:
+        if mask.dtype not in (torch.bool, torch.uint8) or not mask.is_cuda:
+            raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "attention mask must be a bool GPU tensor")
+        m4 = mask
+        while m4.dim() < 4:
+            m4 = m4.unsqueeze(0)
+        m4 = m4.expand(B, Hq, Sq, Skv)
+        m_ptr = m4.data_ptr()
+        m_str = (ctypes_i64 * 4)(*[int(x) for x in m4.stride()])
+    s = torch.cuda.current_stream(query.device).cuda_stream if stream is None else stream
+    _lib.check(_lib.load().biq_attention_burn(
+        s, query.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(),
+        _DTYPE_CODE[query.dtype], B, Hq, Hkv, Sq, Skv, D, _strides_bhsd(query, "query"),
+        _strides_bhsd(key, "key"), _strides_bhsd(value, "value"), _strides_bhsd(out, "output"),
+        m_ptr, m_str, None if attn_bias is None else attn_bias.data_ptr(), int(bool(is_causal)),
+        int(scale is not None), float(scale or 0.0), int(softcap is not None), float(softcap or 0.0)))
     return out
 
 

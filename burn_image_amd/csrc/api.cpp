@@ -108,4 +108,41 @@ int biq_q4_stored_dtype(int layout, int64_t rows, int64_t cols, char *buf, size_
   return BIQ_OK;
 }
 
+// Host-side check of a packed sequence's segment table (the device kernel clamps whatever it reads,
+// but only a valid table gives the per-frame result).
+int biq_check_cu_seqlens(const int32_t *cu, int64_t nseg, int64_t S) {
+  biq::clear_error();
+  if (!cu) return biq::fail(BIQ_ERR_INVALID_ARG, "cu_seqlens is null");
+  if (nseg <= 0) return biq::fail(BIQ_ERR_INVALID_ARG, "segment mask requires at least one segment");
+  if (cu[0] != 0) return biq::fail(BIQ_ERR_INVALID_ARG, "cu_seqlens must start at 0");
+  for (int64_t i = 0; i < nseg; ++i)
+    if (cu[i + 1] <= cu[i])
+      return biq::fail(BIQ_ERR_INVALID_ARG, "cu_seqlens must be strictly ascending (no empty segment)");
+  if ((int64_t)cu[nseg] != S)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "cu_seqlens must end at the sequence length");
+  return BIQ_OK;
+}
+
+// Qwen vision frame ranges (crates/burn_qwen3_vl/src/vision.rs:319-386: `frame_ranges:
+// &[(usize, usize)]`, each frame attends within itself, outputs concatenated in frame order)
+// -> the block-diagonal segment table.  The frames must tile [0, S) in order, each non-empty.
+int biq_frame_ranges_to_cu_seqlens(const int64_t *ranges, int64_t nframes, int64_t S, int32_t *cu) {
+  biq::clear_error();
+  if (!ranges || !cu) return biq::fail(BIQ_ERR_INVALID_ARG, "null pointer argument");
+  if (nframes <= 0) return biq::fail(BIQ_ERR_INVALID_ARG, "at least one frame is required");
+  if (S <= 0 || S > 0x7fffffffLL) return biq::fail(BIQ_ERR_INVALID_ARG, "sequence length out of range");
+  int64_t expect = 0;
+  for (int64_t f = 0; f < nframes; ++f) {
+    const int64_t a = ranges[2 * f], e = ranges[2 * f + 1];
+    if (a != expect) return biq::fail(BIQ_ERR_INVALID_ARG, "frame ranges must be contiguous and start at 0");
+    if (e <= a) return biq::fail(BIQ_ERR_INVALID_ARG, "frame ranges must be non-empty");
+    if (e > S) return biq::fail(BIQ_ERR_INVALID_ARG, "frame range exceeds the sequence");
+    expect = e;
+  }
+  if (expect != S) return biq::fail(BIQ_ERR_INVALID_ARG, "frame ranges must cover the sequence");
+  cu[0] = 0;
+  for (int64_t f = 0; f < nframes; ++f) cu[f + 1] = (int32_t)ranges[2 * f + 1];
+  return BIQ_OK;
+}
+
 }  // extern "C"

@@ -28,7 +28,10 @@ namespace {
 constexpr int BKV = 64;      // keys per LDS tile
 constexpr int VT_LD = BKV + 8;  // halves per row of the transposed V tile
 
-enum MaskMode { MASK_NONE = 0, MASK_CAUSAL = 1, MASK_SEGMENT = 2, MASK_CAUSAL_SEGMENT = 3 };
+// Mask bits: causal (key j > query i masked), segment (block-diagonal over cu_seqlens) and keys
+// (a per-batch byte mask over the key sequence: Qwen's key-padding attention_mask, Burn's
+// key-broadcast bool mask).
+enum MaskMode { MASK_NONE = 0, MASK_CAUSAL = 1, MASK_SEGMENT = 2, MASK_CAUSAL_SEGMENT = 3, MASK_KEYS = 4 };
 
 // Waves per workgroup (each wave owns 32 query rows; two waves per SIMD either way).  Non-causal
 // forms run 8 waves (256 query rows) on each staged K/V tile, so a tile is loaded and written to
@@ -47,6 +50,10 @@ struct AttnArgs {
   int out_dtype;
   const int32_t *cu;
   int64_t nseg;
+  const uint8_t *km;   // key mask bytes [B, Skv] at batch stride km_stride (MASK_KEYS)
+  int64_t km_stride;
+  uint32_t km_drop;    // 1: a nonzero byte masks its key out; 0: a nonzero byte keeps it
+  int fill_mean;       // rows with no visible key: 1 = mean of V over all keys, 0 = zeros
 };
 
 // Load 8 consecutive elements of type InT at p and return them as 8 16-bit values of the
@@ -88,6 +95,7 @@ struct KVRegs {
   static constexpr int V_GROUPS = (BKV / 4) * (DP / 8);       // 4-key x 8-dim V blocks per tile
   u32x4_t k16[K_CHUNKS];  // compute-type bits (f32 inputs are narrowed to f16 at load)
   u32x4_t v16[4];         // input bits (bf16 / f16; f32 inputs narrowed to f16 at load)
+  uint32_t kmb;           // key-mask byte of key tid (wave 0, MASK_KEYS)
 };
 
 // 8 f32 at p -> 8 f16 packed (f32 inputs take the reference's F32 -> F16 bridge at load).
@@ -109,6 +117,7 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
   constexpr int V_GROUPS = KVRegs<DP, InT, NT>::V_GROUPS;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BKV * KS_LD];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[2][DP * VT_LD];
+  __shared__ uint64_t Kbits[2];  // MASK_KEYS: bit t = key t of the staged tile may be attended
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -153,13 +162,18 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
   int64_t kv_begin = 0, kv_end = p.Skv;
   int64_t seg_lo = 0, seg_hi = p.Skv;
   if constexpr (MASK & MASK_SEGMENT) {
+    // Every bound read from cu_seqlens is clamped to [0, Skv] and the range to begin <= end, so
+    // the K/V descriptors below never start before the head or end past it, whatever cu holds
+    // (the binary search itself only ever indexes cu[0 .. nseg]).
+    auto clampk = [&](int64_t x) { return x < 0 ? (int64_t)0 : (x > p.Skv ? p.Skv : x); };
     const int64_t qc = qi < p.Sq ? qi : p.Sq - 1;
     const int64_t sg = segment_of(p.cu, p.nseg, qc);
-    seg_lo = p.cu[sg];
-    seg_hi = p.cu[sg + 1];
+    seg_lo = clampk(p.cu[sg]);
+    seg_hi = clampk(p.cu[sg + 1]);
     const int64_t qlast = (qblk + BQ - 1) < p.Sq ? (qblk + BQ - 1) : p.Sq - 1;
-    kv_begin = p.cu[segment_of(p.cu, p.nseg, qblk)];
-    kv_end = p.cu[segment_of(p.cu, p.nseg, qlast) + 1];
+    kv_begin = clampk(p.cu[segment_of(p.cu, p.nseg, qblk)]);
+    kv_end = clampk(p.cu[segment_of(p.cu, p.nseg, qlast) + 1]);
+    kv_end = kv_end < kv_begin ? kv_begin : kv_end;
   }
   if constexpr (MASK & MASK_CAUSAL) {
     const int64_t qlast = (qblk + BQ - 1) < p.Sq ? (qblk + BQ - 1) : p.Sq - 1;
@@ -222,7 +236,16 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
       return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     }
   };
+  // Key-mask bytes: lane t of wave 0 loads the byte of key kv0 + t (a byte past Skv reads 0; such
+  // keys are outside every visible range anyway).
+  [[maybe_unused]] const uint8_t *kmrow = (MASK & MASK_KEYS) ? p.km + b * p.km_stride : nullptr;
   auto load_tile = [&](int64_t kv0, KVRegs<DP, InT, NT> &R) {
+    if constexpr (MASK & MASK_KEYS) {
+      const int64_t rem = p.Skv - kv0;
+      const uint32_t n = rem <= 0 ? 0u : (rem > 0x7fffffffLL ? 0x7fffffffu : (uint32_t)rem);
+      const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(kmrow + kv0), 0, (int)n, 0x00020000);
+      R.kmb = wave == 0 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0) : 0u;
+    }
     const auto rk = rsrc(kg, kv0, krow_b);
 #pragma unroll
     for (int it = 0; it < K_CHUNKS; ++it) R.k16[it] = load16(rk, koff[it]);
@@ -235,6 +258,12 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
 
   // ---- registers -> LDS buffer: K row-major in the compute type, V transposed f16
   auto store_tile = [&](const KVRegs<DP, InT, NT> &R, int buf) {
+    if constexpr (MASK & MASK_KEYS) {
+      if (wave == 0) {
+        const uint64_t bits = __ballot((R.kmb != 0u) != (p.km_drop != 0u));
+        if (lane == 0) Kbits[buf] = bits;
+      }
+    }
 #pragma unroll
     for (int it = 0; it < K_CHUNKS; ++it) {
       const int c = tid + it * NT;
@@ -322,7 +351,9 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
 
     // ---- mask where the tile needs it; row max of the raw scores (the positive scale commutes
     //      with max, so it is applied once to the maximum and folded into the exponent's FMA)
-    const bool need_mask = kv0 < wave_lo || kv0 + BKV > wave_hi;
+    uint64_t kbits = ~0ull;
+    if constexpr (MASK & MASK_KEYS) kbits = Kbits[buf];
+    const bool need_mask = kv0 < wave_lo || kv0 + BKV > wave_hi || kbits != ~0ull;
     float mx = -INFINITY;
     if (need_mask) {
       // key offsets inside the tile are small: compare in 32 bits against this lane's bounds,
@@ -331,14 +362,18 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
       const int lo = lo64 < -BKV ? -BKV : (lo64 > 2 * BKV ? 2 * BKV : (int)lo64);
       const int hi = hi64 > 2 * BKV ? 2 * BKV : (hi64 < -BKV ? -BKV : (int)hi64);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks) {
+        // this lane's 16 keys of the 32-key half ks sit at bits 8 g + e of m32 (g = r / 4, e = r % 4)
+        const uint32_t m32 = (uint32_t)(kbits >> (32 * ks + 4 * lh));
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kr = 32 * ks + 8 * (r >> 2) + (r & 3);  // key offset without 4 lh
-          const bool ok = kr >= lo && kr < hi;
+          bool ok = kr >= lo && kr < hi;
+          if constexpr (MASK & MASK_KEYS) ok = ok && ((m32 >> (8 * (r >> 2) + (r & 3))) & 1u);
           sacc[ks][r] = ok ? sacc[ks][r] : -INFINITY;
           mx = fmaxf(mx, sacc[ks][r]);
         }
+      }
     } else {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
@@ -398,7 +433,44 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
   // ---- normalise and store O[b, h, qi, d]
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (qi >= p.Sq) return;
+  // Rows with no visible key (only a key mask can empty a row: causal and segment ranges hold the
+  // query's own key).  With fill_mean they take the mean of V over all Skv keys, the softmax of a
+  // row filled with one constant everywhere.  Cold path: the wave sums V cooperatively, lane L
+  // owning dims 2L and 2L + 1, then each empty lane gathers its dims by lane shuffles.
+  [[maybe_unused]] bool empty_row = false;
+  [[maybe_unused]] float mean0 = 0.0f, mean1 = 0.0f;
+  if constexpr (MASK & MASK_KEYS) {
+    empty_row = p.fill_mean && qi < p.Sq && !(l_tot > 0.0f);
+    if (__any(empty_row)) {
+      float s0 = 0.0f, s1 = 0.0f;
+      const int64_t dd = 2 * lane;
+      if (dd < D) {
+        const InT *vc = vg + dd;
+        for (int64_t j = 0; j < p.Skv; ++j) {
+          const InT *e = vc + j * p.vs[2];
+          if constexpr (F32IN) {
+            s0 += e[0];
+            s1 += e[1];
+          } else {
+            const uint32_t w = *reinterpret_cast<const uint32_t *>(e);
+            if constexpr (BF16) {
+              s0 += biq::bf16_lo_to_f32(w);
+              s1 += biq::bf16_hi_to_f32(w);
+            } else {
+              s0 += (float)biq::bitcast<half2_t>(w)[0];
+              s1 += (float)biq::bitcast<half2_t>(w)[1];
+            }
+          }
+        }
+      }
+      const float invn = 1.0f / (float)p.Skv;
+      mean0 = s0 * invn;
+      mean1 = s1 * invn;
+    }
+  }
+  // Lanes past the sequence stay until the end: the empty-row fill gathers dims from every lane.
+  const bool row_in = qi < p.Sq;
+  if (!(MASK & MASK_KEYS) && !row_in) return;
   char *ob = reinterpret_cast<char *>(p.o);
   const int64_t obase = b * p.os[0] + h * p.os[1] + qi * p.os[2];
 #pragma unroll
@@ -407,8 +479,15 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
     for (int g = 0; g < 4; ++g) {
       const int d0 = 32 * i + 8 * g + 4 * lh;
       if (d0 >= D) continue;
-      const float v0 = oacc[i][4 * g] * inv, v1 = oacc[i][4 * g + 1] * inv;
-      const float v2 = oacc[i][4 * g + 2] * inv, v3 = oacc[i][4 * g + 3] * inv;
+      float v0 = oacc[i][4 * g] * inv, v1 = oacc[i][4 * g + 1] * inv;
+      float v2 = oacc[i][4 * g + 2] * inv, v3 = oacc[i][4 * g + 3] * inv;
+      if constexpr (MASK & MASK_KEYS) {
+        // dims d0 .. d0 + 3 live in lanes d0 / 2 (d0, d0 + 1) and d0 / 2 + 1 (d0 + 2, d0 + 3)
+        const float a0 = __shfl(mean0, d0 / 2), a1 = __shfl(mean1, d0 / 2);
+        const float a2 = __shfl(mean0, d0 / 2 + 1), a3 = __shfl(mean1, d0 / 2 + 1);
+        if (empty_row) { v0 = a0; v1 = a1; v2 = a2; v3 = a3; }
+      }
+      if (!row_in) continue;
       if (p.out_dtype == BIQ_DTYPE_F32) {
         float *dst = reinterpret_cast<float *>(ob) + obase + d0;
         *reinterpret_cast<float4 *>(dst) = make_float4(v0, v1, v2, v3);
@@ -425,22 +504,22 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
     }
 }
 
+template <int DP, typename InT, int MASK>
+void launch_one(hipStream_t s, dim3 grid, const AttnArgs &a) {
+  hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK>), grid, dim3(64 * wg_waves(MASK)), 0, s, a);
+}
+
 template <int DP, typename InT>
 void launch_mask(hipStream_t s, dim3 grid, const AttnArgs &a, int mask) {
   switch (mask) {
-    case MASK_NONE:
-      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_NONE>), grid, dim3(64 * wg_waves(MASK_NONE)), 0, s, a);
-      break;
-    case MASK_CAUSAL:
-      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_CAUSAL>), grid, dim3(64 * wg_waves(MASK_CAUSAL)), 0, s, a);
-      break;
-    case MASK_SEGMENT:
-      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_SEGMENT>), grid, dim3(64 * wg_waves(MASK_SEGMENT)), 0, s, a);
-      break;
-    default:
-      hipLaunchKernelGGL((attn_fwd_kernel<DP, InT, MASK_CAUSAL_SEGMENT>), grid,
-                         dim3(64 * wg_waves(MASK_CAUSAL_SEGMENT)), 0, s, a);
-      break;
+    case MASK_NONE: launch_one<DP, InT, MASK_NONE>(s, grid, a); break;
+    case MASK_CAUSAL: launch_one<DP, InT, MASK_CAUSAL>(s, grid, a); break;
+    case MASK_SEGMENT: launch_one<DP, InT, MASK_SEGMENT>(s, grid, a); break;
+    case MASK_CAUSAL_SEGMENT: launch_one<DP, InT, MASK_CAUSAL_SEGMENT>(s, grid, a); break;
+    case MASK_KEYS: launch_one<DP, InT, MASK_KEYS>(s, grid, a); break;
+    case MASK_KEYS | MASK_CAUSAL: launch_one<DP, InT, MASK_KEYS | MASK_CAUSAL>(s, grid, a); break;
+    case MASK_KEYS | MASK_SEGMENT: launch_one<DP, InT, MASK_KEYS | MASK_SEGMENT>(s, grid, a); break;
+    default: launch_one<DP, InT, MASK_KEYS | MASK_CAUSAL_SEGMENT>(s, grid, a); break;
   }
 }
 
@@ -458,7 +537,8 @@ extern "C" int biq_attention(void *stream, const void *q, const void *k, const v
                              int64_t Sq, int64_t Skv, int64_t D, const int64_t *q_strides,
                              const int64_t *k_strides, const int64_t *v_strides,
                              const int64_t *o_strides, float scale, int causal,
-                             const int32_t *cu_seqlens, int64_t nseg) {
+                             const int32_t *cu_seqlens, int64_t nseg, const uint8_t *key_mask,
+                             int64_t key_mask_stride, int key_mask_mode) {
   biq::clear_error();
   if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides)
     return biq::fail(BIQ_ERR_INVALID_ARG, "null pointer argument");
@@ -478,6 +558,11 @@ extern "C" int biq_attention(void *stream, const void *q, const void *k, const v
     return biq::fail(BIQ_ERR_INVALID_ARG, "causal and segment masks require Sq == Skv");
   if (cu_seqlens && nseg <= 0)
     return biq::fail(BIQ_ERR_INVALID_ARG, "segment mask requires at least one segment");
+  if (key_mask && key_mask_mode != BIQ_KEY_MASK_VALID && key_mask_mode != BIQ_KEY_MASK_VALID_FILL_MEAN &&
+      key_mask_mode != BIQ_KEY_MASK_MASKED)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "unknown key mask mode");
+  if (key_mask && key_mask_stride < 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "key mask batch stride must be non-negative");
   const int esz = in_dtype == BIQ_DTYPE_F32 ? 4 : 2;
   const int osz = out_dtype == BIQ_DTYPE_F32 ? 4 : 2;
   const int64_t *st[3] = {q_strides, k_strides, v_strides};
@@ -496,7 +581,7 @@ extern "C" int biq_attention(void *stream, const void *q, const void *k, const v
       return biq::fail(BIQ_ERR_INVALID_ARG, "attention output strides must be multiples of 16 bytes");
   if (k_strides[2] * esz * BKV >= (1LL << 31) || v_strides[2] * esz * BKV >= (1LL << 31))
     return biq::fail(BIQ_ERR_UNSUPPORTED, "attention key/value row stride too large for 32-bit tile offsets");
-  const int mask = (causal ? MASK_CAUSAL : 0) | (cu_seqlens ? MASK_SEGMENT : 0);
+  const int mask = (causal ? MASK_CAUSAL : 0) | (cu_seqlens ? MASK_SEGMENT : 0) | (key_mask ? MASK_KEYS : 0);
   const int64_t bq = 32 * wg_waves(mask);
   if ((Sq + bq - 1) / bq * Hq * B > 0x7fffffffLL)
     return biq::fail(BIQ_ERR_UNSUPPORTED, "attention grid too large");
@@ -512,9 +597,43 @@ extern "C" int biq_attention(void *stream, const void *q, const void *k, const v
   a.out_dtype = out_dtype;
   a.cu = cu_seqlens;
   a.nseg = nseg;
+  a.km = key_mask;
+  a.km_stride = key_mask_stride;
+  a.km_drop = key_mask_mode == BIQ_KEY_MASK_MASKED ? 1u : 0u;
+  a.fill_mean = key_mask_mode == BIQ_KEY_MASK_VALID_FILL_MEAN ? 1 : 0;
   dim3 grid((unsigned)((Sq + bq - 1) / bq * Hq * B));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (D <= 64) launch_dtype<64>(s, grid, a, in_dtype, mask);
   else launch_dtype<128>(s, grid, a, in_dtype, mask);
   return biq::check_launch("attention");
+}
+
+// Burn's ModuleOps::attention (patches/burn-cubecl-0.21.0/src/ops/module.rs:342-367).
+extern "C" int biq_attention_burn(void *stream, const void *q, const void *k, const void *v, void *o,
+                                  int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
+                                  int64_t Skv, int64_t D, const int64_t *q_strides,
+                                  const int64_t *k_strides, const int64_t *v_strides,
+                                  const int64_t *o_strides, const uint8_t *mask,
+                                  const int64_t *mask_strides, const void *attn_bias, int is_causal,
+                                  int has_scale, float scale, int has_softcap, float softcap) {
+  biq::clear_error();
+  (void)softcap;
+  if (attn_bias)
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "attention: an additive attn_bias is not supported by the flash kernel");
+  if (has_softcap)
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "attention: softcap is not supported by the flash kernel");
+  if (has_scale && !(scale > 0.0f))
+    return biq::fail(BIQ_ERR_INVALID_ARG, "attention: an explicit scale must be positive");
+  int64_t km_stride = 0;
+  if (mask) {
+    if (!mask_strides) return biq::fail(BIQ_ERR_INVALID_ARG, "attention: mask strides missing");
+    // only a key-padding mask, broadcast over heads and query rows, maps onto the kernel
+    if (mask_strides[1] != 0 || mask_strides[2] != 0 || (Skv > 1 && mask_strides[3] != 1))
+      return biq::fail(BIQ_ERR_UNSUPPORTED,
+                       "attention: only key-padding masks (broadcast over heads and queries, keys contiguous) are supported");
+    km_stride = B > 1 ? mask_strides[0] : 0;
+  }
+  return biq_attention(stream, q, k, v, o, dtype, dtype, B, Hq, Hkv, Sq, Skv, D, q_strides, k_strides,
+                       v_strides, o_strides, has_scale ? scale : 0.0f, is_causal, nullptr, 0, mask,
+                       km_stride, BIQ_KEY_MASK_MASKED);
 }

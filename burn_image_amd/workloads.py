@@ -184,3 +184,24 @@ def attention_flops(B: int, H: int, D: int, pairs: int) -> float:
 def segment_causal_pairs(cu: np.ndarray) -> int:
     L = np.diff(np.asarray(cu, np.int64))
     return int(np.sum(L * (L + 1) // 2))
+
+
+def c5_padded_attention(heads: int = 32, kv_heads: int = 8, head_dim: int = 128, S: int = 1024,
+                        left_pad: int = 137, right_pad: int = 301):
+    """The C5 shape as a padded batch of two prompts (crates/burn_qwen3_vl/src/processor.rs:
+    379-392): batch 0 left-padded by `left_pad` tokens, batch 1 right-padded by `right_pad`.
+    bf16 Q [2, 32, S, D], K/V [2, 8, S, D] ~ N(0,1) with rotate_half RoPE (theta 5e6) at the
+    valid tokens' positions; returns (q, k, v, key_valid [2, S] bool)."""
+    valid = np.ones((2, S), bool)
+    valid[0, :left_pad] = False
+    valid[1, S - right_pad:] = False
+    pos = np.stack([np.maximum(np.arange(S) - left_pad, 0), np.arange(S)])
+    out = []
+    for i, h in enumerate((heads, kv_heads, kv_heads)):
+        x = rng(5, 8 + i).standard_normal((2, h, S, head_dim), dtype=np.float32)
+        if i < 2:
+            for b in range(2):
+                cos, sin = text_rope_values(pos[b], head_dim, 5.0e6)
+                x[b] = apply_rope_half(x[b], cos, sin)
+        out.append(round_to_bf16(x))
+    return out[0], out[1], out[2], valid

@@ -123,11 +123,23 @@ int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t rows_per_b
                    float branch_eps, const float *gate, float *x_out, const float *next_gamma,
                    float next_eps, const float *next_scale, void *next_out, int next_dtype);
 
+/* Key-mask modes of biq_attention (the byte mask is [B, Skv], one byte per key).
+ * BIQ_KEY_MASK_VALID: a nonzero byte marks a key that may be attended (Qwen's `attention_mask`,
+ *   crates/burn_qwen3_vl/src/text.rs:163-170); a query row left with no visible key is zero.
+ * BIQ_KEY_MASK_VALID_FILL_MEAN: as VALID, but a row with no visible key gets the mean of V over
+ *   all Skv keys -- what the reference's `mask_fill(-1e30)` then softmax gives for such a row
+ *   (text.rs:176-178: every score equal, uniform weights), e.g. the left-padding rows of a batch.
+ * BIQ_KEY_MASK_MASKED: a nonzero byte masks its key out (Burn's bool attention mask polarity);
+ *   a row with no visible key is zero. */
+#define BIQ_KEY_MASK_VALID 0
+#define BIQ_KEY_MASK_VALID_FILL_MEAN 1
+#define BIQ_KEY_MASK_MASKED 2
+
 /* Exact attention O = softmax(Q K^T * scale + mask) V, the operator behind
  * AttentionKernel::execute / execute_gqa (crates/burn_boogu/src/model/attention.rs:47-105), the
- * padded-blackbox flash kernel (native_flash.rs:1006-1090) and Burn's attention op
- * (patches/burn-cubecl-0.21.0/src/ops/module.rs:342-367), plus Qwen's causal text attention
- * (crates/burn_qwen3_vl/src/text.rs:103-192) and per-frame vision attention (vision.rs:319-388).
+ * padded-blackbox flash kernel (native_flash.rs:1006-1090), plus Qwen's causal text attention with
+ * its key-padding mask (crates/burn_qwen3_vl/src/text.rs:103-192) and per-frame vision attention
+ * (vision.rs:319-388).
  *   q: [B, Hq, Sq, D] addressed by q_strides = {batch, head, seq} element strides (D contiguous),
  *   k, v: [B, Hkv, Skv, D] with their strides, o: [B, Hq, Sq, D] with o_strides.  Token-major
  *   [B, S, H, D] tensors are passed with strides {S*H*D, D, H*D}.
@@ -137,8 +149,13 @@ int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t rows_per_b
  *   e.g. the released D = 120 without a padded copy).
  *   scale: softmax scale; scale <= 0 selects 1/sqrt(D).
  *   causal != 0: key j is masked for query i when j > i (requires Sq == Skv).
- *   cu_seqlens (device int32[nseg + 1], ascending, cu[0] = 0, cu[nseg] = Sq) or NULL: block-
- *   diagonal segment mask over a packed sequence (requires Sq == Skv).
+ *   cu_seqlens (device int32[nseg + 1]) or NULL: block-diagonal segment mask over a packed
+ *   sequence (requires Sq == Skv).  A valid table starts at 0, ascends strictly and ends at Sq
+ *   (biq_check_cu_seqlens checks a host copy); the kernel clamps every bound it reads to [0, Skv],
+ *   so a malformed table never reads outside K/V, but its rows are then unspecified.
+ *   key_mask (device bytes; row b at key_mask + b * key_mask_stride, Skv bytes each; stride 0
+ *   broadcasts one row over the batch) or NULL, interpreted by key_mask_mode (BIQ_KEY_MASK_*);
+ *   combines with causal and segment masks.
  * Arithmetic: Q K^T on the matrix cores in bf16 (bf16 inputs) or f16 (f16 and f32 inputs, as the
  * reference's F32->F16 bridge, attention.rs:406-497), f32 online softmax, P and V in f16 on the
  * matrix cores, f32 accumulation. */
@@ -146,7 +163,38 @@ int biq_attention(void *stream, const void *q, const void *k, const void *v, voi
                   int in_dtype, int out_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
                   int64_t Skv, int64_t D, const int64_t *q_strides, const int64_t *k_strides,
                   const int64_t *v_strides, const int64_t *o_strides, float scale, int causal,
-                  const int32_t *cu_seqlens, int64_t nseg);
+                  const int32_t *cu_seqlens, int64_t nseg, const uint8_t *key_mask,
+                  int64_t key_mask_stride, int key_mask_mode);
+
+/* Burn's attention op, ModuleOps::attention(q, k, v, mask: Option<Bool>, attn_bias,
+ * AttentionModuleOptions { is_causal, scale, softcap })
+ * (patches/burn-cubecl-0.21.0/src/ops/module.rs:342-367), over the same kernel.  Tensors and
+ * strides as biq_attention, with q, k, v and o all of `dtype`.
+ *   mask: NULL, or a bool tensor [B, H, Sq, Skv] (true = masked out) given by its element strides
+ *   mask_strides[4] (0 = broadcast).  Only a key-padding mask -- broadcast over heads and query
+ *   rows (strides[1] == strides[2] == 0), keys contiguous -- maps onto the kernel; any other mask
+ *   returns BIQ_ERR_UNSUPPORTED.  A query row with every key masked is zero.
+ *   attn_bias != NULL or has_softcap != 0: BIQ_ERR_UNSUPPORTED (the reference sends these to
+ *   Burn's dense fallback; this library has none).
+ *   has_scale != 0: softmax scale `scale` (> 0); otherwise 1/sqrt(D).
+ *   is_causal: key j > query i masked (requires Sq == Skv).
+ * The reference's callers pass no mask, bias or softcap (native_flash.rs:905-912,2745-2820). */
+int biq_attention_burn(void *stream, const void *q, const void *k, const void *v, void *o,
+                       int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Skv,
+                       int64_t D, const int64_t *q_strides, const int64_t *k_strides,
+                       const int64_t *v_strides, const int64_t *o_strides, const uint8_t *mask,
+                       const int64_t *mask_strides, const void *attn_bias, int is_causal,
+                       int has_scale, float scale, int has_softcap, float softcap);
+
+/* Host-only check of a segment table: cu[0] == 0, cu strictly ascending, cu[nseg] == S
+ * (BIQ_ERR_INVALID_ARG otherwise, with the reason in biq_last_error()). */
+int biq_check_cu_seqlens(const int32_t *cu, int64_t nseg, int64_t S);
+
+/* Host-only: Qwen vision frame ranges `&[(usize, usize)]` (crates/burn_qwen3_vl/src/vision.rs:
+ * 319-386), given as int64 pairs ranges[2 f], ranges[2 f + 1], -> the segment table
+ * cu[nframes + 1] biq_attention takes.  The frames must tile [0, S) in order, each non-empty
+ * (the reference's per-frame loop concatenates the frame outputs in order). */
+int biq_frame_ranges_to_cu_seqlens(const int64_t *ranges, int64_t nframes, int64_t S, int32_t *cu);
 
 /* Fused attention-input preparation: strict-F32 RMSNorm of Q and K rows, Boogu interleaved-pair
  * RoPE on both, and the cast of Q, K and V to the attention operand type, in one pass.

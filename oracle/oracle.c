@@ -264,10 +264,16 @@ static inline int visible(int64_t i, int64_t j, int causal, const int32_t *cu, i
  * rounded to the kernel's input dtype), out [B, Hq, nrows, Dv] double.  GQA maps query head h to
  * key/value head h / (Hq / Hkv) (attention.rs:67-105 materialised `repeat_dim`).  Masked scores are
  * excluded exactly (Qwen fills -1e30 before softmax, whose weight underflows to 0 in f32).
+ * key_valid: NULL or [B, Skv] bytes, nonzero = the key may be attended: Qwen's key-padding
+ * `attention_mask`, OR-ed into the causal mask as `valid.bool_not()` broadcast over queries
+ * (crates/burn_qwen3_vl/src/text.rs:163-176).  A row left with no visible key gets, with
+ * fill_mean, the mean of V over all Skv keys (softmax of a row filled with -1e30 everywhere is
+ * uniform, text.rs:176-178), and zeros without it.
  * rows: query indices evaluated (NULL = all Sq). */
 void orc_attention_f64(const float *q, const float *k, const float *v, int64_t B, int64_t Hq,
                        int64_t Hkv, int64_t Sq, int64_t Skv, int64_t D, int64_t Dv, double scale,
-                       int causal, const int32_t *cu_seqlens, int64_t nseg, const int64_t *rows,
+                       int causal, const int32_t *cu_seqlens, int64_t nseg,
+                       const uint8_t *key_valid, int fill_mean, const int64_t *rows,
                        int64_t nrows, double *out) {
     int64_t group = Hq / Hkv;
     #pragma omp parallel for collapse(2) schedule(dynamic, 1)
@@ -282,7 +288,8 @@ void orc_attention_f64(const float *q, const float *k, const float *v, int64_t B
             double *s = (double *)malloc(sizeof(double) * (size_t)Skv);
             double mx = -INFINITY;
             for (int64_t j = 0; j < Skv; ++j) {
-                if (!visible(i, j, causal, cu_seqlens, nseg)) { s[j] = -INFINITY; continue; }
+                if (!visible(i, j, causal, cu_seqlens, nseg) ||
+                    (key_valid && !key_valid[b * Skv + j])) { s[j] = -INFINITY; continue; }
                 double acc = 0.0;
                 for (int64_t d = 0; d < D; ++d) acc += (double)qr[d] * (double)kb[j * D + d];
                 s[j] = acc * scale;
@@ -294,6 +301,13 @@ void orc_attention_f64(const float *q, const float *k, const float *v, int64_t B
                 denom += s[j];
             }
             for (int64_t d = 0; d < Dv; ++d) o[d] = 0.0;
+            if (mx == -INFINITY) {  /* no visible key */
+                if (fill_mean)
+                    for (int64_t j = 0; j < Skv; ++j)
+                        for (int64_t d = 0; d < Dv; ++d) o[d] += (double)vb[j * Dv + d] / (double)Skv;
+                free(s);
+                continue;
+            }
             for (int64_t j = 0; j < Skv; ++j) {
                 if (s[j] == 0.0) continue;
                 double p = s[j] / denom;

@@ -58,7 +58,7 @@ def lib():
         L.orc_effective_query_chunk.argtypes = [I64, I64]
         L.orc_effective_query_chunk.restype = I64
         L.orc_attention_f64.argtypes = [P, P, P, I64, I64, I64, I64, I64, I64, I64, ctypes.c_double,
-                                        ctypes.c_int, P, I64, P, I64, P]
+                                        ctypes.c_int, P, I64, P, ctypes.c_int, P, I64, P]
         L.orc_attention_f64.restype = None
         L.orc_cpu_attention_f32.argtypes = [P, P, P, I64, I64, I64, I64, I64, I64, I64,
                                             ctypes.c_float, I64, I64, P]
@@ -174,8 +174,11 @@ def effective_query_chunk(query_len: int, requested: int) -> int:
     return int(lib().orc_effective_query_chunk(query_len, requested))
 
 
-def attention_f64(q, k, v, scale=None, causal=False, cu_seqlens=None, rows=None):
-    """Exact float64 attention over [B, H, S, D] inputs (GQA when k/v have fewer heads)."""
+def attention_f64(q, k, v, scale=None, causal=False, cu_seqlens=None, rows=None, key_valid=None,
+                  fill_mean=False):
+    """Exact float64 attention over [B, H, S, D] inputs (GQA when k/v have fewer heads).
+    key_valid: optional [B, Skv] bool (True = the key may be attended, Qwen's attention_mask);
+    rows left without a visible key get mean(V) with `fill_mean` (text.rs:176-178), else 0."""
     q = _c(q, np.float32)
     k = _c(k, np.float32)
     v = _c(v, np.float32)
@@ -189,9 +192,10 @@ def attention_f64(q, k, v, scale=None, causal=False, cu_seqlens=None, rows=None)
     out = np.zeros((B, Hq, nrows, Dv), np.float64)
     cu = None if cu_seqlens is None else _c(cu_seqlens, np.int32)
     nseg = 0 if cu is None else cu.size - 1
+    kv = None if key_valid is None else _c(np.asarray(key_valid).reshape(B, Skv) != 0, np.uint8)
     lib().orc_attention_f64(_p(q), _p(k), _p(v), B, Hq, Hkv, Sq, Skv, D, Dv, float(scale), int(causal),
-                            None if cu is None else _p(cu), nseg, None if idx is None else _p(idx),
-                            nrows, _p(out))
+                            None if cu is None else _p(cu), nseg, None if kv is None else _p(kv),
+                            int(bool(fill_mean)), None if idx is None else _p(idx), nrows, _p(out))
     return out
 
 
@@ -312,8 +316,11 @@ def np_q4_dequant(words, scales, layout: int, block: int, K: int, N: int) -> np.
     return (qn * s).astype(np.float32)
 
 
-def np_attention(q, k, v, scale=None, causal=False, cu_seqlens=None):
-    """Dense float64 softmax(Q K^T s) V with optional causal / segment masks and GQA."""
+def np_attention(q, k, v, scale=None, causal=False, cu_seqlens=None, key_valid=None,
+                 fill_value=None):
+    """Dense float64 softmax(Q K^T s) V with optional causal / segment / key-padding masks and
+    GQA.  Masked scores become -inf, or `fill_value` when given (Qwen's mask_fill(-1e30),
+    text.rs:176: a row with every key masked then averages V over all keys)."""
     q = np.asarray(q, np.float64)
     k = np.asarray(k, np.float64)
     v = np.asarray(v, np.float64)
@@ -330,7 +337,10 @@ def np_attention(q, k, v, scale=None, causal=False, cu_seqlens=None):
     if cu_seqlens is not None:
         seg = np.searchsorted(np.asarray(cu_seqlens), np.arange(Sq), side="right") - 1
         mask &= seg[:, None] == seg[None, :]
-    s = np.where(mask, s, -np.inf)
+    mask = np.broadcast_to(mask, (B, 1) + mask.shape)
+    if key_valid is not None:
+        mask = mask & (np.asarray(key_valid, bool).reshape(B, 1, 1, -1))
+    s = np.where(mask, s, -np.inf if fill_value is None else float(fill_value))
     s = s - s.max(axis=-1, keepdims=True)
     p = np.exp(s)
     p /= p.sum(axis=-1, keepdims=True)

@@ -65,9 +65,73 @@ def test_attention_validation_fails_closed(args, needle):
     dummy = ctypes.c_void_p(256)
     rc = lib.biq_attention(None, dummy, dummy, dummy, dummy, _lib.DTYPE_BF16, _lib.DTYPE_F32,
                            p["B"], p["Hq"], p["Hkv"], p["Sq"], p["Skv"], p["D"], st, st, st, st,
-                           0.0, p["causal"], None, 0)
+                           0.0, p["causal"], None, 0, None, 0, 0)
     assert rc != _lib.OK
     assert needle in lib.biq_last_error()
+
+
+def test_burn_attention_op_rejects_bias_softcap_and_general_masks():
+    """ModuleOps::attention (patches/burn-cubecl-0.21.0/src/ops/module.rs:342-367): the flash
+    kernel takes no additive bias, no softcap and no mask other than key padding; each returns
+    BIQ_ERR_UNSUPPORTED before any GPU work (the reference routes them to a dense fallback)."""
+    from burn_image_amd import _lib
+    lib = _lib.load()
+    st = _lib.strides3((1, 1, 64))
+    d = ctypes.c_void_p(256)
+    I4 = ctypes.c_int64 * 4
+
+    def call(mask=None, mstr=None, bias=None, softcap=None, scale=None):
+        return lib.biq_attention_burn(None, d, d, d, d, _lib.DTYPE_F16, 2, 4, 4, 8, 8, 64, st, st, st, st,
+                                      mask, mstr, bias, 0, int(scale is not None), float(scale or 0.0),
+                                      int(softcap is not None), float(softcap or 0.0))
+
+    assert call(bias=d) == _lib.ERR_UNSUPPORTED and b"attn_bias" in lib.biq_last_error()
+    assert call(softcap=30.0) == _lib.ERR_UNSUPPORTED and b"softcap" in lib.biq_last_error()
+    # a full [B, H, Sq, Skv] mask, a per-head mask and a per-query mask cannot run
+    for strides in ((256, 64, 8, 1), (8, 8, 0, 1), (64, 0, 8, 1)):
+        assert call(mask=d, mstr=I4(*strides)) == _lib.ERR_UNSUPPORTED
+        assert b"key-padding" in lib.biq_last_error()
+    assert call(scale=-1.0) == _lib.ERR_INVALID_ARG
+
+
+def test_attention_key_mask_mode_validation():
+    from burn_image_amd import _lib
+    lib = _lib.load()
+    st = _lib.strides3((1, 1, 64))
+    d = ctypes.c_void_p(256)
+    rc = lib.biq_attention(None, d, d, d, d, _lib.DTYPE_BF16, _lib.DTYPE_F32, 1, 4, 2, 8, 8, 64, st, st, st,
+                           st, 0.0, 0, None, 0, d, 8, 7)
+    assert rc == _lib.ERR_INVALID_ARG and b"key mask mode" in lib.biq_last_error()
+
+
+@pytest.mark.parametrize("cu,S,ok", [
+    ([0, 4, 8], 8, True),
+    ([0, 8], 8, True),
+    ([1, 4, 8], 8, False),      # does not start at 0
+    ([0, 4, 4, 8], 8, False),   # empty segment
+    ([0, 6, 4, 8], 8, False),   # descending
+    ([0, 4, 7], 8, False),      # does not end at S
+    ([0, -4, 8], 8, False),     # negative bound
+    ([0, 4, 9], 8, False),      # past the sequence
+])
+def test_cu_seqlens_host_validator(cu, S, ok):
+    """Host-side segment table check (a malformed table never reaches the kernel through the
+    Python API; vision.rs:319-325 holds its frame ranges on the host)."""
+    import burn_image_amd as B
+    if ok:
+        B.check_cu_seqlens(cu, S)
+    else:
+        with pytest.raises(B.InvalidArgument):
+            B.check_cu_seqlens(cu, S)
+
+
+def test_frame_ranges_to_cu_seqlens():
+    """vision.rs:319-386 frame ranges -> segment table, and the contract's failures."""
+    import burn_image_amd as B
+    assert list(B.frame_ranges_to_cu_seqlens([(0, 3), (3, 10), (10, 16)], 16)) == [0, 3, 10, 16]
+    for bad in ([(0, 3), (4, 16)], [(0, 3), (3, 3), (3, 16)], [(0, 3), (3, 12)], [(1, 16)], [(0, 17)]):
+        with pytest.raises(B.InvalidArgument):
+            B.frame_ranges_to_cu_seqlens(bad, 16)
 
 
 def test_q4_linear_validation_fails_closed():

@@ -223,3 +223,67 @@ def test_gpu_many_items_ragged_keys(gpu, oracle, odt):
         assert_parity(host(out), host(full), "many_items_full_vs_fp32")
     else:
         assert np.max(np.abs(got - ref)) <= np.max(np.abs(ref)) * 2.0 ** -7 + 2e-3
+
+
+# ---------------------------------------------------------------------------------------------
+# key masks (Qwen attention_mask, Burn key-padding masks) and wider mask coverage
+# ---------------------------------------------------------------------------------------------
+
+def test_gpu_c5_padded_batch_key_mask(gpu, oracle):
+    """C5 geometry (Hq 32, Hkv 8, D 128, S 1024) as a B = 2 padded batch: left padding in batch
+    0, right padding in batch 1, causal GQA with the key-padding mask (text.rs:146-185).  Rows of
+    batch 0 before its first valid token see no key: with the -1e30 fill mode they average V
+    over every key, as the reference computes them."""
+    q, k, v, valid = W.c5_padded_attention()
+    qd, kd, vd = (dev(a, torch.bfloat16, gpu) for a in (q, k, v))
+    vm = torch.from_numpy(valid).to(gpu)
+    out = B.attention(qd, kd, vd, is_causal=True, key_mask=vm,
+                      key_mask_mode=B._lib.KEY_MASK_VALID_FILL_MEAN, out_dtype=torch.float32)
+    ref = oracle.attention_f64(q, k, v, causal=True, key_valid=valid, fill_mean=True).astype(np.float32)
+    assert_parity(host(out), ref, "c5_padded_causal_fill_mean")
+    # zero mode: identical except the empty rows, which are exactly zero
+    out0 = B.attention(qd, kd, vd, is_causal=True, key_mask=vm.to(torch.uint8), out_dtype=torch.float32)
+    ref0 = oracle.attention_f64(q, k, v, causal=True, key_valid=valid).astype(np.float32)
+    assert_parity(host(out0), ref0, "c5_padded_causal_zero")
+    assert torch.count_nonzero(out0[0, :, :137]).item() == 0
+    assert torch.equal(out0[:, :, 137:][0], out[0, :, 137:]) and torch.equal(out0[1], out[1])
+    # Burn polarity (True = masked) through the op mirror gives the zero-mode result bitwise
+    outb = B.burn_attention(qd, kd, vd, (~vm)[:, None, None, :], is_causal=True)
+    assert torch.equal(outb.float(), out0.to(torch.bfloat16).float())
+
+
+@pytest.mark.parametrize("mode", ["keys", "keys_segment", "keys_causal_segment"])
+def test_gpu_key_mask_combinations(gpu, oracle, mode):
+    """Key masks on the unmasked 8-wave, per-segment 8-wave and causal 4-wave forms (f16, GQA
+    4:2, D 128, B 2), with masked keys scattered (not only padding)."""
+    rng = np.random.default_rng(31)
+    S = 700
+    q, k, v = (W.round_to_f16(rng.standard_normal((2, h, S, 128), dtype=np.float32)) for h in (4, 2, 2))
+    valid = rng.random((2, S)) < 0.7
+    cu = np.array([0, 90, 300, 301, 700], np.int32)
+    causal = mode == "keys_causal_segment"
+    seg = None if mode == "keys" else cu
+    qd, kd, vd = (dev(a, torch.float16, gpu) for a in (q, k, v))
+    out = B.attention(qd, kd, vd, is_causal=causal, cu_seqlens=seg, key_mask=torch.from_numpy(valid).to(gpu),
+                      key_mask_mode=B._lib.KEY_MASK_VALID_FILL_MEAN, out_dtype=torch.float32)
+    ref = oracle.attention_f64(q, k, v, causal=causal, cu_seqlens=seg, key_valid=valid,
+                               fill_mean=True).astype(np.float32)
+    assert_parity(host(out), ref, f"key_mask_{mode}")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("D", [64, 120])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gpu_segment_masks_dtypes_widths_batches(gpu, oracle, dtype, D, causal):
+    """Per-segment masks (8-wave form) and causal + segment (4-wave form) for f16 and f32 inputs,
+    D in {64, 120} and B = 2 (the per-segment 8-wave form's register-set and V-group variants)."""
+    rng = np.random.default_rng(40 + D + (1 if causal else 0))
+    S = 640
+    rnd = W.round_to_f16 if dtype == "f16" else (lambda a: a)
+    q, k, v = (rnd(rng.standard_normal((2, h, S, D), dtype=np.float32)) for h in (4, 2, 2))
+    cu = np.array([0, 64, 70, 333, 512, 640], np.int32)
+    tdt = torch.float16 if dtype == "f16" else torch.float32
+    qd, kd, vd = (dev(a, tdt, gpu) for a in (q, k, v))
+    out = B.attention(qd, kd, vd, is_causal=causal, cu_seqlens=cu, out_dtype=torch.float32)
+    ref = oracle.attention_f64(q, k, v, causal=causal, cu_seqlens=cu).astype(np.float32)
+    assert_parity(host(out), ref, f"segment_{dtype}_D{D}_causal{int(causal)}")

@@ -164,3 +164,63 @@ def test_c5_segment_generator_properties_correctness():
     L = np.diff(cu)
     assert cu[0] == 0 and cu[-1] == 1024
     assert np.all(L >= 64) and np.all(L <= 512)
+
+
+def test_key_mask_equals_attention_over_kept_keys_correctness(oracle):
+    """Qwen's key-padding mask (text.rs:163-170): masked keys contribute nothing, so the result
+    equals attention over the kept keys alone (non-causal; GQA 4:2)."""
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((2, 4, 12, 16)).astype(np.float32)
+    k = rng.standard_normal((2, 2, 20, 16)).astype(np.float32)
+    v = rng.standard_normal((2, 2, 20, 16)).astype(np.float32)
+    valid = rng.random((2, 20)) < 0.6
+    valid[:, 3] = True
+    out = oracle.attention_f64(q, k, v, key_valid=valid)
+    for b in range(2):
+        keep = np.nonzero(valid[b])[0]
+        alone = oracle.attention_f64(q[b:b + 1], k[b:b + 1][:, :, keep], v[b:b + 1][:, :, keep])
+        assert np.max(np.abs(out[b:b + 1] - alone)) < 1e-12
+    dense = oracle.np_attention(q, k, v, key_valid=valid)
+    assert np.max(np.abs(out - dense)) < 1e-12
+
+
+def test_key_mask_left_padding_causal_rows_correctness(oracle):
+    """Left padding (processor.rs:379-385) under the causal mask: row i >= pad equals causal
+    attention over keys [pad, i]; rows i < pad see no key and average V over every key with the
+    reference's -1e30 fill (text.rs:176-178), or are zero without it."""
+    rng = np.random.default_rng(12)
+    S, pad = 10, 3
+    q = rng.standard_normal((1, 2, S, 8)).astype(np.float32)
+    k = rng.standard_normal((1, 2, S, 8)).astype(np.float32)
+    v = rng.standard_normal((1, 2, S, 8)).astype(np.float32)
+    valid = np.ones((1, S), bool)
+    valid[0, :pad] = False
+    filled = oracle.attention_f64(q, k, v, causal=True, key_valid=valid, fill_mean=True)
+    zeroed = oracle.attention_f64(q, k, v, causal=True, key_valid=valid)
+    tail = oracle.attention_f64(q[:, :, pad:], k[:, :, pad:], v[:, :, pad:], causal=True)
+    assert np.max(np.abs(filled[:, :, pad:] - tail)) < 1e-12
+    assert np.array_equal(filled[:, :, pad:], zeroed[:, :, pad:])
+    mean_v = v.astype(np.float64).mean(axis=2, keepdims=True)
+    assert np.max(np.abs(filled[:, :, :pad] - mean_v)) < 1e-12
+    assert np.all(zeroed[:, :, :pad] == 0.0)
+    # the literal statement: scores filled with -1e30 before a dense softmax
+    literal = oracle.np_attention(q, k, v, causal=True, key_valid=valid, fill_value=-1.0e30)
+    assert np.max(np.abs(filled - literal)) < 1e-12
+
+
+def test_key_mask_with_segments_and_right_padding_correctness(oracle):
+    """Right padding plus per-frame segments: padded keys drop out of their segment only."""
+    rng = np.random.default_rng(13)
+    cu = np.array([0, 5, 12], np.int32)
+    q = rng.standard_normal((2, 2, 12, 8)).astype(np.float32)
+    k = rng.standard_normal((2, 2, 12, 8)).astype(np.float32)
+    v = rng.standard_normal((2, 2, 12, 8)).astype(np.float32)
+    valid = np.ones((2, 12), bool)
+    valid[1, 9:] = False
+    for causal in (False, True):
+        a = oracle.attention_f64(q, k, v, causal=causal, cu_seqlens=cu, key_valid=valid)
+        b = oracle.np_attention(q, k, v, causal=causal, cu_seqlens=cu, key_valid=valid)
+        assert np.max(np.abs(a - b)) < 1e-12
+    # batch 0 has no padding: identical to the unmasked call
+    a0 = oracle.attention_f64(q[:1], k[:1], v[:1], cu_seqlens=cu, key_valid=valid[:1])
+    assert np.array_equal(a0, oracle.attention_f64(q[:1], k[:1], v[:1], cu_seqlens=cu))
