@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libbiq.so")
 
-SOURCES = ["api.cpp", "q4_format.hip", "q4_gemm.hip", "q4_gemv.hip", "attention.hip", "qk_prep.hip", "block_glue.hip"]
+SOURCES = ["api.cpp", "q4_format.hip", "q4_gemm.hip", "q4_gemv.hip", "attention.hip", "qk_prep.hip", "block_glue.hip", "noalloc.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc" if os.path.exists("/opt/rocm/bin/hipcc") else "hipcc")
 ARCH = "gfx950"

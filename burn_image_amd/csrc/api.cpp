@@ -56,6 +56,16 @@ int stream_workspace(hipStream_t s, size_t bytes, void **out) {
   return BIQ_OK;
 }
 
+int get_scratch(hipStream_t s, const Scratch *fixed, size_t bytes, void **out) {
+  if (fixed == nullptr) return stream_workspace(s, bytes, out);
+  if (bytes > fixed->bytes)
+    return fail(BIQ_ERR_UNSUPPORTED, "this call needs " + std::to_string(bytes) +
+                                         " bytes of scratch; the static scratch holds " +
+                                         std::to_string(fixed->bytes));
+  *out = fixed->ptr;
+  return BIQ_OK;
+}
+
 int device_cu_count() {
   static std::mutex m;
   static std::map<int, int> cache;

@@ -32,6 +32,14 @@ int fail(int status, const std::string &msg);
 int check_launch(const char *what);
 // Device scratch owned by the library for (current device, stream s), at least `bytes` long.
 int stream_workspace(hipStream_t s, size_t bytes, void **out);
+// A caller-fixed scratch region (device address and size) for launches that must not allocate.
+struct Scratch {
+  void *ptr;
+  size_t bytes;
+};
+// Scratch of `bytes` for a launch on stream s: the fixed region when `fixed` is given (and large
+// enough: BIQ_ERR_UNSUPPORTED otherwise), else the library's grow-only per-stream workspace.
+int get_scratch(hipStream_t s, const Scratch *fixed, size_t bytes, void **out);
 // Compute units of the current device.
 int device_cu_count();
 

@@ -688,7 +688,7 @@ SkPlan plan_tail(int64_t T, int64_t units, int64_t granule, int cus) {
 
 template <class GG, int LAYOUT, int XMODE, int B, bool GLU>
 int launch_geo(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const float *bias,
-               void *y, int y_dtype, int64_t M, int64_t N, int64_t K) {
+               void *y, int y_dtype, int64_t M, int64_t N, int64_t K, const biq::Scratch *scr) {
   constexpr int BNO = GLU ? GG::BN / 2 : GG::BN;
   constexpr int64_t UNIT = (int64_t)(B >= GG::BK ? B : GG::BK);
   const int tiles_m = (int)((M + GG::BM - 1) / GG::BM), tiles_n = (int)((N + BNO - 1) / BNO);
@@ -699,7 +699,7 @@ int launch_geo(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const
   if (plan.sk_wgs > 0) {
     void *part = nullptr;
     const size_t chunks = (size_t)tail * plan.parts;
-    const int st = biq::stream_workspace(s, chunks * GG::BM * GG::BN * sizeof(float), &part);
+    const int st = biq::get_scratch(s, scr, chunks * GG::BM * GG::BN * sizeof(float), &part);
     if (st != BIQ_OK) return st;
     plan.part = reinterpret_cast<float *>(part);
   }
@@ -722,30 +722,31 @@ int launch_geo(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const
 
 template <int LAYOUT, int XMODE, bool GLU>
 int launch_blk(hipStream_t s, int block, const void *x, int64_t ldx, const Q4Args &w,
-               const float *bias, void *y, int y_dtype, int64_t M, int64_t N, int64_t K) {
+               const float *bias, void *y, int y_dtype, int64_t M, int64_t N, int64_t K,
+               const biq::Scratch *scr) {
   using G8 = GemmGeo<XMODE, 8>;
   using G16 = GemmGeo<XMODE, 16>;
   using G = GemmGeo<XMODE, 128>;
   switch (block) {
-    case 8: return launch_geo<G8, LAYOUT, XMODE, 8, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K);
-    case 16: return launch_geo<G16, LAYOUT, XMODE, 16, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K);
-    case 32: return launch_geo<G, LAYOUT, XMODE, 32, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K);
-    case 64: return launch_geo<G, LAYOUT, XMODE, 64, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K);
-    default: return launch_geo<G, LAYOUT, XMODE, 128, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K);
+    case 8: return launch_geo<G8, LAYOUT, XMODE, 8, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+    case 16: return launch_geo<G16, LAYOUT, XMODE, 16, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+    case 32: return launch_geo<G, LAYOUT, XMODE, 32, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+    case 64: return launch_geo<G, LAYOUT, XMODE, 64, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+    default: return launch_geo<G, LAYOUT, XMODE, 128, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
   }
 }
 
 template <int LAYOUT, bool GLU>
 int launch_layout(hipStream_t s, int x_dtype, int block, const void *x, int64_t ldx,
                   const Q4Args &w, const float *bias, void *y, int y_dtype, int64_t M, int64_t N,
-                  int64_t K) {
+                  int64_t K, const biq::Scratch *scr) {
   switch (x_dtype) {
     case BIQ_DTYPE_BF16:
-      return launch_blk<LAYOUT, XM_BF16, GLU>(s, block, x, ldx, w, bias, y, y_dtype, M, N, K);
+      return launch_blk<LAYOUT, XM_BF16, GLU>(s, block, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
     case BIQ_DTYPE_F16:
-      return launch_blk<LAYOUT, XM_F16, GLU>(s, block, x, ldx, w, bias, y, y_dtype, M, N, K);
+      return launch_blk<LAYOUT, XM_F16, GLU>(s, block, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
     default:
-      return launch_blk<LAYOUT, XM_F32, GLU>(s, block, x, ldx, w, bias, y, y_dtype, M, N, K);
+      return launch_blk<LAYOUT, XM_F32, GLU>(s, block, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
   }
 }
 
@@ -754,7 +755,7 @@ int launch_layout(hipStream_t s, int x_dtype, int block, const void *x, int64_t 
 namespace biq {
 int q4_gemv_launch(hipStream_t s, const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                    const uint32_t *words, const float *scales, int layout, int block, int64_t N,
-                   const float *bias, float *y);
+                   const float *bias, float *y, const Scratch *scr);
 }
 
 namespace {
@@ -794,22 +795,32 @@ int check_linear(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx, 
 
 }  // namespace
 
-extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K,
-                             int64_t ldx, const uint32_t *words, const float *scales, int layout,
-                             int block, int64_t N, const float *bias, void *y, int y_dtype) {
-  biq::clear_error();
+namespace biq {
+// biq_q4_linear with its scratch taken from `scr` (NULL: the library's per-stream workspace).
+int q4_linear_launch(void *stream, const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                     const uint32_t *words, const float *scales, int layout, int block, int64_t N,
+                     const float *bias, void *y, int y_dtype, const Scratch *scr) {
   const int st = check_linear(x, x_dtype, M, K, ldx, words, scales, layout, block, N, y, y_dtype);
   if (st != BIQ_OK) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // Up to 16 rows with an f32 output stream the weights through the small-M kernel
   // (q4_gemv.hip): split-K over the whole chip instead of N / 256 workgroups of 128 rows.
   if (M <= 16 && y_dtype == BIQ_DTYPE_F32)
-    return biq::q4_gemv_launch(s, x, x_dtype, M, K, ldx, words, scales, layout, block, N, bias,
-                               reinterpret_cast<float *>(y));
+    return q4_gemv_launch(s, x, x_dtype, M, K, ldx, words, scales, layout, block, N, bias,
+                          reinterpret_cast<float *>(y), scr);
   const Q4Args w{words, nullptr, scales, nullptr};
   if (layout == BIQ_Q4_KN_AXIS1)
-    return launch_layout<BIQ_Q4_KN_AXIS1, false>(s, x_dtype, block, x, ldx, w, bias, y, y_dtype, M, N, K);
-  return launch_layout<BIQ_Q4_NK_AXIS0, false>(s, x_dtype, block, x, ldx, w, bias, y, y_dtype, M, N, K);
+    return launch_layout<BIQ_Q4_KN_AXIS1, false>(s, x_dtype, block, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+  return launch_layout<BIQ_Q4_NK_AXIS0, false>(s, x_dtype, block, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+}
+}  // namespace biq
+
+extern "C" int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K,
+                             int64_t ldx, const uint32_t *words, const float *scales, int layout,
+                             int block, int64_t N, const float *bias, void *y, int y_dtype) {
+  biq::clear_error();
+  return biq::q4_linear_launch(stream, x, x_dtype, M, K, ldx, words, scales, layout, block, N, bias, y,
+                               y_dtype, nullptr);
 }
 
 extern "C" int biq_q4_linear_swiglu(void *stream, const void *x, int x_dtype, int64_t M, int64_t K,
@@ -824,6 +835,6 @@ extern "C" int biq_q4_linear_swiglu(void *stream, const void *x, int x_dtype, in
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const Q4Args w{words1, words3, scales1, scales3};
   if (layout == BIQ_Q4_KN_AXIS1)
-    return launch_layout<BIQ_Q4_KN_AXIS1, true>(s, x_dtype, block, x, ldx, w, nullptr, y, y_dtype, M, N, K);
-  return launch_layout<BIQ_Q4_NK_AXIS0, true>(s, x_dtype, block, x, ldx, w, nullptr, y, y_dtype, M, N, K);
+    return launch_layout<BIQ_Q4_KN_AXIS1, true>(s, x_dtype, block, x, ldx, w, nullptr, y, y_dtype, M, N, K, nullptr);
+  return launch_layout<BIQ_Q4_NK_AXIS0, true>(s, x_dtype, block, x, ldx, w, nullptr, y, y_dtype, M, N, K, nullptr);
 }

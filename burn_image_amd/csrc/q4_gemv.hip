@@ -346,7 +346,7 @@ namespace biq {
 // Small-M route of biq_q4_linear (f32 output).  Returns a BIQ_* status.
 int q4_gemv_launch(hipStream_t s, const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                    const uint32_t *words, const float *scales, int layout, int block, int64_t N,
-                   const float *bias, float *y) {
+                   const float *bias, float *y, const Scratch *scr) {
   const bool kn = layout == BIQ_Q4_KN_AXIS1;
   const int64_t slab = kn ? KN_SLAB : NK_SLAB;
   const int64_t unit = kn ? 32 * KN_BATCH : 128 * NK_BATCH;  // a multiple of every block size
@@ -369,7 +369,7 @@ int q4_gemv_launch(hipStream_t s, const void *x, int x_dtype, int64_t M, int64_t
   float *part = nullptr;
   if (ksplit > 1) {
     void *ws = nullptr;
-    const int st = stream_workspace(s, (size_t)(ksplit * M * N) * sizeof(float), &ws);
+    const int st = get_scratch(s, scr, (size_t)(ksplit * M * N) * sizeof(float), &ws);
     if (st != BIQ_OK) return st;
     part = reinterpret_cast<float *>(ws);
   }

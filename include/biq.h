@@ -97,6 +97,23 @@ int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K
                   const uint32_t *words, const float *scales, int layout, int block, int64_t N,
                   const float *bias, void *y, int y_dtype);
 
+/* Size of the static scratch biq_q4_linear_noalloc uses on each GPU (32 MiB). */
+#define BIQ_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* biq_q4_linear for callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  No counterpart in the reference.  Same
+ * arguments, kernels, work split and (bitwise) results as biq_q4_linear, but it calls no
+ * hipMalloc / hipFree or other allocating routine: the partial sums of K-split tail tiles and of
+ * the small-M route live in a static device array of BIQ_NOALLOC_SCRATCH_BYTES that each GPU
+ * running the library holds until the process ends.  A call whose work split needs more scratch
+ * returns BIQ_ERR_UNSUPPORTED before any GPU work (the message gives both sizes).  The array is
+ * shared by every call on that GPU and keeps the last call's contents (each call writes every
+ * element it reads): calls that overlap on one GPU -- on different streams, or from threads
+ * without ordering -- race. */
+int biq_q4_linear_noalloc(void *stream, const void *x, int x_dtype, int64_t M, int64_t K,
+                          int64_t ldx, const uint32_t *words, const float *scales, int layout,
+                          int block, int64_t N, const float *bias, void *y, int y_dtype);
+
 /* y[M, N] = silu(x . W1) * (x . W3), the gated half of the SwiGLU feed-forward
  * `silu(linear_1(x)) * linear_3(x)` (crates/burn_boogu/src/model/feed_forward.rs:32-36), whose
  * output feeds linear_2.  One pass over x computes both projections (same layout, block, K and N;
