@@ -99,10 +99,14 @@ __device__ __forceinline__ void f32x8_to_f16_split_slots(const float4 &a, const 
 }
 
 // Tile geometry: a wave owns WM x WN MFMA tiles of 32 x 32; the workgroup holds WAVES_M x WAVES_N
-// waves.
-template <int WM_, int WN_, int WAVES_M_, int WAVES_N_, int BK_>
+// waves.  RESCALE selects how block scales are applied (see the kernel): false keeps each block's
+// partial sum in its own accumulator and adds scale * partial at the block's end; true rescales
+// the running accumulator at each block boundary, which halves the accumulator registers and so
+// leaves room for the 128-row wave tile.
+template <int WM_, int WN_, int WAVES_M_, int WAVES_N_, int BK_, bool RESCALE_ = false>
 struct Geo {
   static constexpr int WM = WM_, WN = WN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr bool RESCALE = RESCALE_;
   static constexpr int BK = BK_;        // K per LDS stage
   static constexpr int A_LD = BK + 8;   // LDS row stride of the activation tile, in halves
   static constexpr int BM = 32 * WM * WAVES_M, BN = 32 * WN * WAVES_N;
@@ -125,15 +129,33 @@ struct Geo {
 #endif
 template <int XMODE, int BLK>
 using GemmGeo = Geo<BIQ_GEMM_WAVES, (XMODE == XM_F32 || BLK <= 16) ? 64 : BIQ_GEMM_BK>;
+// Large workgroup tile for 16-bit activations and blocks >= 32: 8 waves in a 2 x 4 grid of
+// 128 x 64 wave tiles -> 256 x 256, K staged 64 at a time (two 45 KB LDS buffers).  A decoded
+// weight fragment feeds four MFMAs instead of two and each staged activation / weight byte serves
+// twice the output of the 128 x 256 tile; block scales use the running rescale.  Measured
+// against 128 x 256 at 4608 rows: 3072x3072 -8%, 3072x12288 -3%, 12288x3072 -5% time, 3072x9216
+// level (648 tiles leave the last of three rounds half idle) -- launch_blk picks per shape.
+using GemmGeoBig = Geo<4, 2, 2, 4, 64, true>;
 
 // Register sets of the global -> LDS pipeline (see the kernel): two for 16-bit activations,
 // blocks of 128 and the [K/8, N] word layout; one where a second set would not fit the 256
 // registers without spilling.
-template <int LAYOUT, int XMODE, int BLK>
-constexpr int PF_SETS = (LAYOUT == BIQ_Q4_KN_AXIS1 && XMODE != XM_F32 && BLK >= 128) ? 2 : 1;
+// The large tile keeps one set (a second does not fit its registers).
+template <class G, int LAYOUT, int XMODE, int BLK>
+constexpr int PF_SETS = (!G::RESCALE && LAYOUT == BIQ_Q4_KN_AXIS1 && XMODE != XM_F32 && BLK >= 128) ? 2 : 1;
 // K units a tail part starts on a multiple of (see the kernel's paired loop)
-template <int LAYOUT, int XMODE, int BLK, int BK>
-constexpr int PART_GRANULE = (PF_SETS<LAYOUT, XMODE, BLK> == 2 && BLK <= BK) ? 2 : 1;
+template <class G, int LAYOUT, int XMODE, int BLK>
+constexpr int PART_GRANULE = (PF_SETS<G, LAYOUT, XMODE, BLK> == 2 && BLK <= G::BK) ? 2 : 1;
+
+// Running-rescale form: block scales enter as t = s with |t| clamped to [2^-60, 2^60], so that
+// the ratio of two consecutive scales stays finite.  Scales the importer writes (max|w| / 7, or
+// f32::MIN_POSITIVE for an all-zero block, whose nibbles are all zero) are exact up to the clamp;
+// a block of zero scale contributes q * 2^-60 * x instead of 0.  NaN stays NaN.
+__device__ __forceinline__ float clamp_scale(float s) {
+  const float a = fabsf(s);
+  const float c = a < 0x1p-60f ? 0x1p-60f : (a > 0x1p60f ? 0x1p60f : a);
+  return (a != a) ? s : (s < 0.0f ? -c : c);
+}
 
 // Per-thread register copy of one tile's global data.
 template <class G, int XMODE, int NSC>
@@ -306,7 +328,7 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   const int64_t pid = tail_wg ? sk.dp_tiles + t_tail : first;
   // with two register sets, tail parts start on even K tiles, so every part but the last (which
   // ends at K) has an even number of tiles for the paired loop below
-  constexpr int64_t GRAN = PART_GRANULE<LAYOUT, XMODE, BLK, G::BK>;
+  constexpr int64_t GRAN = PART_GRANULE<G, LAYOUT, XMODE, BLK>;
   auto part_start = [&](int64_t kp) {
     return kp >= sk.parts ? units : GRAN * (kp * (units / GRAN) / sk.parts);
   };
@@ -481,7 +503,17 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     }
   };
 
-  floatx16_t acc[WM][WN], part[WM][WN];
+  // Block scales.  Partial form: the MFMAs of block b accumulate part = sum_k x q in their own
+  // registers, then acc += s_b * part.  Rescale form (G::RESCALE): the MFMAs accumulate straight
+  // into acc, which is kept relative to the current block's scale: at the first step of block b,
+  // acc *= t_{b-1} / t_b, and at the end acc *= t_last, so acc = sum_b t_b * part_b.  The same one
+  // VALU op per accumulator per block, half the registers; the relative rounding of the ratios and
+  // multiplies is ~2^-24 per block of the partial output, far inside the f32 parity gate.
+  constexpr bool RESC = G::RESCALE;
+  floatx16_t acc[WM][WN], part[RESC ? 1 : WM][RESC ? 1 : WN];
+  [[maybe_unused]] float t_prev[WN];
+#pragma unroll
+  for (int j = 0; j < WN; ++j) t_prev[j] = 1.0f;
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -507,7 +539,7 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   // register is never copied while its load is in flight (a copy would make the wave wait for
   // it).  Two sets where the registers allow it without spilling in the loop, else one.  The
   // block scales travel in the same sets.
-  constexpr int PF = PF_SETS<LAYOUT, XMODE, BLK>;
+  constexpr int PF = PF_SETS<G, LAYOUT, XMODE, BLK>;
   constexpr int NTT = (PF == 2 || TPB == 2) ? 2 : 1;  // K tiles per loop iteration
   TileRegs<G, XMODE, TILE_BLOCKS> RS[PF];
   float sc_hold[WN][TILE_BLOCKS];  // scales of the tile computed next, copied out of its set
@@ -590,20 +622,42 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
           const bool first = BLK >= BK ? (tt % TPB == 0 && s == 0) : (s % SPB) == 0;
           const bool last = BLK >= BK ? (tt % TPB == TPB - 1 && s == BK / 16 - 1) : (s % SPB) == SPB - 1;
           const int tb = BLK >= BK ? 0 : s / SPB;
+          if constexpr (RESC) {
+            // acc starts at zero and t_prev at 1, so the first block's ratio (finite: clamped
+            // scales) leaves it zero
+            float r[WN];
+            if (first) {
 #pragma unroll
-          for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j) {
-              floatx16_t p =
-                  biq::mfma32x32x16_f16(a_cur[i][0], b_cur[j], first ? biq::zero16() : part[i][j]);
-              if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a_cur[i][1], b_cur[j], p);
-              part[i][j] = p;
+              for (int j = 0; j < WN; ++j) {
+                const float t = clamp_scale(sc_cur[j][tb]);
+                r[j] = t_prev[j] / t;
+                t_prev[j] = t;
+              }
             }
-          if (last) {
 #pragma unroll
             for (int i = 0; i < WM; ++i)
 #pragma unroll
-              for (int j = 0; j < WN; ++j) acc[i][j] += sc_cur[j][tb] * part[i][j];
+              for (int j = 0; j < WN; ++j) {
+                floatx16_t c = acc[i][j];
+                if (first) c *= r[j];
+                acc[i][j] = biq::mfma32x32x16_f16(a_cur[i][0], b_cur[j], c);
+              }
+          } else {
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+              for (int j = 0; j < WN; ++j) {
+                floatx16_t p =
+                    biq::mfma32x32x16_f16(a_cur[i][0], b_cur[j], first ? biq::zero16() : part[i][j]);
+                if constexpr (NSPLIT == 2) p = biq::mfma32x32x16_f16(a_cur[i][1], b_cur[j], p);
+                part[i][j] = p;
+              }
+            if (last) {
+#pragma unroll
+              for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j) acc[i][j] += sc_cur[j][tb] * part[i][j];
+            }
           }
         }
 
@@ -622,6 +676,12 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   }
 
   // ---------------- epilogue: bias (or the SwiGLU gate), convert, store ---------------------
+  if constexpr (RESC) {
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j) acc[i][j] *= t_prev[j];
+  }
   if (ku0 == 0 && ku1 == units) {  // the whole K of the tile
     store_tile_out<G, GLU>(acc, m0, n0, bias, yv, y_dtype, M, N);
     continue;
@@ -660,8 +720,9 @@ struct Q4Args {
 // choice: 1024x4096x4096 (128 tiles) 79.5 -> 57.2 us with 2 parts (chosen); 1024x4096x6144 (192
 // tiles) and the 4608-row O / MLP shapes are fastest whole (chosen); 4608x3072x9216: 6 parts
 // (chosen) 403 us, 8 parts 400 us, whole 423 us.
-SkPlan plan_tail(int64_t T, int64_t units, int64_t granule, int cus) {
+SkPlan plan_tail(int64_t T, int64_t units, int64_t granule, int cus, double *est_rounds = nullptr) {
   SkPlan p{(int)T, 0, 1, units, nullptr};
+  if (est_rounds) *est_rounds = cus > 0 ? (double)((T + cus - 1) / cus) : 1.0;
   const char *env = getenv("BIQ_GEMM_STREAMK");
   const int forced = env ? atoi(env) : -1;
   if (cus <= 0 || units < 2 || forced == 0 || forced == 1) return p;
@@ -679,6 +740,10 @@ SkPlan plan_tail(int64_t T, int64_t units, int64_t granule, int cus) {
     }
   }
   if (forced > 1) parts = forced < max_parts ? forced : (int)max_parts;
+  if (est_rounds) {
+    const int64_t rounds = (tail * parts + cus - 1) / cus;
+    *est_rounds = (double)(T / cus) + (parts > 1 ? rounds * (1.0 / parts + 0.13) + 0.012 * parts : 1.0);
+  }
   if (parts <= 1) return p;
   p.dp_tiles = (int)(T - tail);
   p.parts = parts;
@@ -693,7 +758,7 @@ int launch_geo(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const
   constexpr int64_t UNIT = (int64_t)(B >= GG::BK ? B : GG::BK);
   const int tiles_m = (int)((M + GG::BM - 1) / GG::BM), tiles_n = (int)((N + BNO - 1) / BNO);
   const int64_t T = (int64_t)tiles_m * tiles_n;
-  SkPlan plan = plan_tail(T, (K + UNIT - 1) / UNIT, PART_GRANULE<LAYOUT, XMODE, B, GG::BK>,
+  SkPlan plan = plan_tail(T, (K + UNIT - 1) / UNIT, PART_GRANULE<GG, LAYOUT, XMODE, B>,
                          biq::device_cu_count());
   const int tail = (int)(T - plan.dp_tiles);
   if (plan.sk_wgs > 0) {
@@ -720,19 +785,49 @@ int launch_geo(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const
   return biq::check_launch(GLU ? "q4 linear swiglu" : "q4 linear");
 }
 
+// Estimated launch time of geometry GG in units of one 128 x 256 tile: rounds of tiles over the
+// CUs (with the tail split the way launch_geo would split it) times the cost of one tile.  A
+// 256 x 256 tile costs 1.86 units (measured: 7% less per output than two 128 x 256 tiles).
+template <class GG, int LAYOUT, int XMODE, int B, bool GLU>
+double est_launch(int64_t M, int64_t N, int64_t K) {
+  constexpr int BNO = GLU ? GG::BN / 2 : GG::BN;
+  constexpr int64_t UNIT = (int64_t)(B >= GG::BK ? B : GG::BK);
+  const int64_t T = ((M + GG::BM - 1) / GG::BM) * ((N + BNO - 1) / BNO);
+  double rounds = 1.0;
+  plan_tail(T, (K + UNIT - 1) / UNIT, PART_GRANULE<GG, LAYOUT, XMODE, B>, biq::device_cu_count(), &rounds);
+  return rounds * (GG::RESCALE ? 1.86 : 1.0);
+}
+
+// BIQ_GEMM_TILE in the environment: "small" or "big" forces the 128 x 256 or the 256 x 256
+// geometry where both apply (a tuning switch); otherwise est_launch decides.
+template <int LAYOUT, int XMODE, int B, bool GLU>
+int launch_pick(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const float *bias, void *y,
+                int y_dtype, int64_t M, int64_t N, int64_t K, const biq::Scratch *scr) {
+  using GS = GemmGeo<XMODE, B>;
+  if constexpr (XMODE != XM_F32 && B >= 32) {
+    const char *env = getenv("BIQ_GEMM_TILE");
+    bool big;
+    if (env && env[0] == 's') big = false;
+    else if (env && env[0] == 'b') big = true;
+    else big = est_launch<GemmGeoBig, LAYOUT, XMODE, B, GLU>(M, N, K) <
+               est_launch<GS, LAYOUT, XMODE, B, GLU>(M, N, K);
+    if (big) return launch_geo<GemmGeoBig, LAYOUT, XMODE, B, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+  }
+  return launch_geo<GS, LAYOUT, XMODE, B, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+}
+
 template <int LAYOUT, int XMODE, bool GLU>
 int launch_blk(hipStream_t s, int block, const void *x, int64_t ldx, const Q4Args &w,
                const float *bias, void *y, int y_dtype, int64_t M, int64_t N, int64_t K,
                const biq::Scratch *scr) {
   using G8 = GemmGeo<XMODE, 8>;
   using G16 = GemmGeo<XMODE, 16>;
-  using G = GemmGeo<XMODE, 128>;
   switch (block) {
     case 8: return launch_geo<G8, LAYOUT, XMODE, 8, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
     case 16: return launch_geo<G16, LAYOUT, XMODE, 16, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
-    case 32: return launch_geo<G, LAYOUT, XMODE, 32, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
-    case 64: return launch_geo<G, LAYOUT, XMODE, 64, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
-    default: return launch_geo<G, LAYOUT, XMODE, 128, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+    case 32: return launch_pick<LAYOUT, XMODE, 32, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+    case 64: return launch_pick<LAYOUT, XMODE, 64, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+    default: return launch_pick<LAYOUT, XMODE, 128, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
   }
 }
 
