@@ -798,20 +798,49 @@ double est_launch(int64_t M, int64_t N, int64_t K) {
   return rounds * (GG::RESCALE ? 1.86 : 1.0);
 }
 
-// BIQ_GEMM_TILE in the environment: "small" or "big" forces the 128 x 256 or the 256 x 256
-// geometry where both apply (a tuning switch); otherwise est_launch decides.
+// Geometry choice.  Where the 256 x 256 tile applies, the rows may also be split: rows
+// [0, M_big) run as 256 x 256 tiles and the rest as 128 x 256 tiles, in two launches on the
+// stream, with M_big (a multiple of 256, possibly 0 or M) minimising the summed est_launch.  E.g.
+// 4608 x 3072 x 9216: 3584 rows of 256 x 256 tiles fill two rounds (504 tiles) and the last
+// 1024 rows (288 tiles of 128 x 256) finish in a little over one round of half-size tiles,
+// where either tile alone leaves most of a round idle.  Rows of the two parts are rounded in a
+// different order (partial vs rescale form): equal within the parity gate, not bitwise.
+// BIQ_GEMM_TILE in the environment: "small" or "big" forces one geometry for all rows (a tuning
+// switch); BIQ_GEMM_STREAMK=0 ("every tile owned") also keeps the rows unsplit.
 template <int LAYOUT, int XMODE, int B, bool GLU>
 int launch_pick(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const float *bias, void *y,
                 int y_dtype, int64_t M, int64_t N, int64_t K, const biq::Scratch *scr) {
   using GS = GemmGeo<XMODE, B>;
+  using GB = GemmGeoBig;
   if constexpr (XMODE != XM_F32 && B >= 32) {
     const char *env = getenv("BIQ_GEMM_TILE");
-    bool big;
-    if (env && env[0] == 's') big = false;
-    else if (env && env[0] == 'b') big = true;
-    else big = est_launch<GemmGeoBig, LAYOUT, XMODE, B, GLU>(M, N, K) <
-               est_launch<GS, LAYOUT, XMODE, B, GLU>(M, N, K);
-    if (big) return launch_geo<GemmGeoBig, LAYOUT, XMODE, B, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
+    const char *sk = getenv("BIQ_GEMM_STREAMK");
+    const bool no_split = sk && (sk[0] == '0' || sk[0] == '1') && sk[1] == 0;
+    int64_t m_big = 0;
+    if (env && env[0] == 's') {
+      m_big = 0;
+    } else if (env && env[0] == 'b') {
+      m_big = M;
+    } else {
+      double best = est_launch<GS, LAYOUT, XMODE, B, GLU>(M, N, K);
+      const double whole_big = est_launch<GB, LAYOUT, XMODE, B, GLU>(M, N, K);
+      if (whole_big < best) { best = whole_big; m_big = M; }
+      if (!no_split)
+        for (int64_t mb = GB::BM; mb < M; mb += GB::BM) {
+          const double e = est_launch<GB, LAYOUT, XMODE, B, GLU>(mb, N, K) +
+                           est_launch<GS, LAYOUT, XMODE, B, GLU>(M - mb, N, K);
+          if (e < best - 0.02) { best = e; m_big = mb; }
+        }
+    }
+    if (m_big > 0) {
+      const int st = launch_geo<GB, LAYOUT, XMODE, B, GLU>(s, x, ldx, w, bias, y, y_dtype, m_big, N, K, scr);
+      if (st != BIQ_OK || m_big == M) return st;
+      const int esz = XMODE == XM_F32 ? 4 : 2;
+      const int osz = y_dtype == BIQ_DTYPE_F32 ? 4 : 2;
+      return launch_geo<GS, LAYOUT, XMODE, B, GLU>(s, reinterpret_cast<const char *>(x) + m_big * ldx * esz, ldx,
+                                                   w, bias, reinterpret_cast<char *>(y) + m_big * N * osz, y_dtype,
+                                                   M - m_big, N, K, scr);
+    }
   }
   return launch_geo<GS, LAYOUT, XMODE, B, GLU>(s, x, ldx, w, bias, y, y_dtype, M, N, K, scr);
 }
