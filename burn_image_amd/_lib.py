@@ -41,8 +41,9 @@ SIGNATURES = {
     "biq_q4_quantize": ([_P, _P, _I, _I64, _I64, _P, _P], _I),
     "biq_q4_dequant_f32": ([_P, _P, _P, _I, _I, _I64, _I64, _P], _I),
     "biq_q4_linear": ([_P, _P, _I, _I64, _I64, _I64, _P, _P, _I, _I, _I64, _P, _P, _I], _I),
-    "biq_block_glue": ([_P, _I64, _I64, _I64, _P, _P, _I, _P, ctypes.c_float, _P, _P, _P, ctypes.c_float,
-                        _P, _P, _I], _I),
+    "biq_block_glue": ([_P, _I64, _I64, _I64, _P, _P, _I, _P, _P, _P, ctypes.c_float, _P, _P, _P,
+                        ctypes.c_float, _P, _P, _I], _I),
+    "biq_silu": ([_P, _I64, _P, _I, _P], _I),
     "biq_q4_linear_noalloc": ([_P, _P, _I, _I64, _I64, _I64, _P, _P, _I, _I, _I64, _P, _P, _I], _I),
     "biq_q4_linear_swiglu": ([_P, _P, _I, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _I], _I),
     "biq_attention": ([_P, _P, _P, _P, _P, _I, _I, _I64, _I64, _I64, _I64, _I64, _I64,

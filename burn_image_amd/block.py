@@ -1,10 +1,10 @@
 """The modulated Boogu DiT block on libbiq: projections, attention, feed-forward and the fused
 row-wise glue, composed as the reference composes them.
 
-Mirrors crates/burn_boogu/src/model/block.rs:84-134 (SingleStreamBlock, modulated branch),
-norm.rs:101-153 (RmsNormZero), attention.rs:700-833 (GqaAttention) and feed_forward.rs:5-37
-(LuminaFeedForward).  Every product and reduction runs in a libbiq kernel; torch only holds the
-buffers (and applies the one-row silu of the conditioning vector, norm.rs:147).
+Mirrors crates/burn_boogu/src/model/block.rs:84-134 (SingleStreamBlock, modulated branch) and
+:138-350 (DoubleStreamBlock), norm.rs:101-153 (RmsNormZero), attention.rs:499-833
+(DoubleStreamAttention, GqaAttention) and feed_forward.rs:5-37 (LuminaFeedForward).  Every
+product, reduction and activation runs in a libbiq kernel; torch only allocates the buffers.
 """
 from __future__ import annotations
 
@@ -25,11 +25,12 @@ def block_glue(branch: torch.Tensor, *, residual: Optional[torch.Tensor] = None,
                branch_norm: Optional[RmsNorm] = None, gate: Optional[torch.Tensor] = None,
                residual_out: Optional[torch.Tensor] = None, next_norm: Optional[RmsNorm] = None,
                next_scale: Optional[torch.Tensor] = None, next_dtype: Optional[torch.dtype] = None,
+               branch_scale: Optional[torch.Tensor] = None, branch_shift: Optional[torch.Tensor] = None,
                stream: Optional[int] = None) -> Optional[torch.Tensor]:
-    """One fused glue pass over [B, S, W] rows (block.rs:91-111):
-    r = residual + rmsnorm(branch) * tanh(gate) (or r = branch without a residual), written to
-    `residual_out` (may be `residual`); with `next_dtype`, returns
-    rmsnorm(r) * (1 + next_scale) in that dtype.  gate / next_scale are [B, W] rows."""
+    """One fused glue pass over [B, S, W] rows (block.rs:91-111, 248-350):
+    u = branch * (1 + branch_scale) + branch_shift; r = residual + rmsnorm(u) * tanh(gate) (or
+    r = u without a residual), written to `residual_out` (may be `residual`); with `next_dtype`,
+    returns rmsnorm(r) * (1 + next_scale) in that dtype.  gate / scales / shift are [B, W] rows."""
     if branch.dim() != 3:
         raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "block glue works on [B, S, W] tokens")
     B, S, Wd = branch.shape
@@ -39,24 +40,42 @@ def block_glue(branch: torch.Tensor, *, residual: Optional[torch.Tensor] = None,
     for name, t in (("residual", residual), ("residual_out", residual_out)):
         if t is not None and t.dtype != torch.float32:
             raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, f"{name} is the f32 residual stream")
-    for name, t in (("gate", gate), ("next_scale", next_scale)):
+    for name, t in (("gate", gate), ("next_scale", next_scale), ("branch_scale", branch_scale),
+                    ("branch_shift", branch_shift)):
         if t is not None and tuple(t.shape) != (B, Wd):
             raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, f"{name} must be [B, W]")
     f32 = lambda t: None if t is None else t.to(torch.float32).contiguous()  # noqa: E731
     g_b = f32(branch_norm.gamma) if branch_norm is not None else None
     g_n = f32(next_norm.gamma) if next_norm is not None else None
     gate_c, scale_c = f32(gate), f32(next_scale)
+    bsc_c, bsh_c = f32(branch_scale), f32(branch_shift)
     nxt = None
     if next_dtype is not None:
         nxt = torch.empty((B, S, Wd), dtype=next_dtype, device=branch.device)
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     s = torch.cuda.current_stream(branch.device).cuda_stream if stream is None else stream
     _lib.check(_lib.load().biq_block_glue(
-        s, B * S, Wd, S, ptr(residual), branch.data_ptr(), _DTYPE_CODE[branch.dtype], ptr(g_b),
+        s, B * S, Wd, S, ptr(residual), branch.data_ptr(), _DTYPE_CODE[branch.dtype], ptr(bsc_c), ptr(bsh_c),
+        ptr(g_b),
         branch_norm.epsilon if branch_norm is not None else 0.0, ptr(gate_c), ptr(residual_out),
         ptr(g_n), next_norm.epsilon if next_norm is not None else 0.0, ptr(scale_c), ptr(nxt),
         _DTYPE_CODE[next_dtype] if next_dtype is not None else 0))
     return nxt
+
+
+def silu(x: torch.Tensor, stream: Optional[int] = None) -> torch.Tensor:
+    """f32 silu(x) = x / (1 + e^-x) on the GPU (libbiq biq_silu)."""
+    x = x.contiguous()
+    y = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    s = torch.cuda.current_stream(x.device).cuda_stream if stream is None else stream
+    _lib.check(_lib.load().biq_silu(s, x.numel(), x.data_ptr(), _DTYPE_CODE[x.dtype], y.data_ptr()))
+    return y
+
+
+def modulation_rows(linear: Linear, conditioning: torch.Tensor, width: int, parts: int = 4):
+    """linear(silu(conditioning)) split into `parts` [B, width] views (norm.rs:144-151)."""
+    mod = linear_forward(linear, silu(conditioning))
+    return tuple(mod[:, i * width:(i + 1) * width] for i in range(parts))
 
 
 @dataclass
@@ -67,8 +86,9 @@ class RmsNormZero:
     norm: RmsNorm
 
     def modulation(self, conditioning: torch.Tensor, width: int):
-        mod = linear_forward(self.linear, torch.nn.functional.silu(conditioning.to(torch.float32)))
-        return tuple(mod[:, i * width:(i + 1) * width] for i in range(4))
+        """The four [B, W] rows of linear(silu(conditioning)) (norm.rs:144-151), silu in libbiq."""
+        return tuple(t.contiguous() for t in
+                     modulation_rows(self.linear, conditioning, width, 4))
 
 
 @dataclass
@@ -130,3 +150,166 @@ class SingleStreamBlock:
         out = torch.empty_like(tokens)
         block_glue(mlp, residual=tokens1, branch_norm=self.ffn_norm2, gate=gate_mlp, residual_out=out)
         return out
+
+
+# ---------------------------------------------------------------------------------------------
+# dual-stream attention and block (the released model's leading layers)
+# ---------------------------------------------------------------------------------------------
+
+def _project_rows_into(lin: Linear, x: torch.Tensor, out: torch.Tensor, row0: int) -> None:
+    """out[b, row0:row0 + S_x] = linear(x[b]) for every batch element, written in place (the
+    reference's Tensor::cat along tokens, attention.rs:646-668, without a concatenation copy)."""
+    Bn, Sx, _ = x.shape
+    N = out.shape[-1]
+    if Bn == 1 or out.shape[1] == Sx:
+        dst = out[:, row0:row0 + Sx]
+        if dst.is_contiguous():
+            linear_forward(lin, x, out=dst.view(Bn * Sx, N))
+            return
+    for b in range(Bn):
+        linear_forward(lin, x[b], out=out[b, row0:row0 + Sx])
+
+
+def _rows(x: torch.Tensor, row0: int, n: int):
+    """[B, n, W] token range of x as GEMM inputs: one strided view when B == 1, else per batch."""
+    return [x[b, row0:row0 + n] for b in range(x.shape[0])]
+
+
+@dataclass
+class DoubleStreamAttention:
+    """Joint instruction/image attention with per-stream projections (attention.rs:499-720):
+    instruct_to_{q,k,v} and img_to_{q,k,v} project the two streams, the projections are joined
+    along tokens as [instruction, image], normalised and rotated per head, attended jointly
+    (grouped-query), split back, projected by instruct_out / img_out and finally by the shared
+    to_out -- per stream (split) or jointly, as the kernel's SPLIT_DOUBLE_STREAM_SHARED_PROJECTION
+    says (project_shared_output, attention.rs:700-720).  Returns (image, instruction)."""
+    img_to_q: Linear
+    img_to_k: Linear
+    img_to_v: Linear
+    instruct_to_q: Linear
+    instruct_to_k: Linear
+    instruct_to_v: Linear
+    img_out: Linear
+    instruct_out: Linear
+    to_out: Linear
+    norm_q: RmsNorm
+    norm_k: RmsNorm
+    heads: int
+    kv_heads: int
+    head_dim: int
+    query_chunk_size: int = 8192
+    kernel: type = NativeQ4FlashAttention
+
+    def forward(self, image: torch.Tensor, instruction: torch.Tensor,
+                rope: Tuple[torch.Tensor, torch.Tensor]):
+        Bn, Si, _ = image.shape
+        St = instruction.shape[1]
+        S = St + Si
+        dev = image.device
+        q = torch.empty((Bn, S, self.heads * self.head_dim), dtype=torch.float32, device=dev)
+        k = torch.empty((Bn, S, self.kv_heads * self.head_dim), dtype=torch.float32, device=dev)
+        v = torch.empty_like(k)
+        for dst, lin_t, lin_i in ((q, self.instruct_to_q, self.img_to_q), (k, self.instruct_to_k, self.img_to_k),
+                                  (v, self.instruct_to_v, self.img_to_v)):
+            _project_rows_into(lin_t, instruction, dst, 0)
+            _project_rows_into(lin_i, image, dst, St)
+        attended = self.kernel.execute_gqa_with_qk_norm_rope(
+            q.view(Bn, S, self.heads, self.head_dim), k.view(Bn, S, self.kv_heads, self.head_dim),
+            v.view(Bn, S, self.kv_heads, self.head_dim), self.norm_q, self.norm_k, rope,
+            self.query_chunk_size).reshape(Bn, S, self.heads * self.head_dim)
+        width = self.img_out.weight.N
+        instr = torch.empty((Bn, St, width), dtype=torch.float32, device=dev)
+        img = torch.empty((Bn, Si, width), dtype=torch.float32, device=dev)
+        for b, rows in enumerate(_rows(attended, 0, St)):
+            linear_forward(self.instruct_out, rows, out=instr[b])
+        for b, rows in enumerate(_rows(attended, St, Si)):
+            linear_forward(self.img_out, rows, out=img[b])
+        return self.project_shared_output(instr, img, self.kernel.SPLIT_DOUBLE_STREAM_SHARED_PROJECTION)
+
+    def project_shared_output(self, instruction: torch.Tensor, image: torch.Tensor, split_streams: bool):
+        """to_out per stream (split) or on the token-joined streams; both return (image,
+        instruction) and are equal, to_out being row-wise (attention.rs:700-720)."""
+        if split_streams:
+            return linear_forward(self.to_out, image), linear_forward(self.to_out, instruction)
+        Bn, St, W = instruction.shape
+        Si = image.shape[1]
+        joined = torch.empty((Bn, St + Si, W), dtype=instruction.dtype, device=instruction.device)
+        joined[:, :St].copy_(instruction)
+        joined[:, St:].copy_(image)
+        merged = linear_forward(self.to_out, joined)
+        return merged[:, St:], merged[:, :St]
+
+
+@dataclass
+class DoubleStreamBlock:
+    """The leading dual-stream block (block.rs:138-350) on libbiq kernels.  Image and
+    instruction keep separate residual streams: joint attention over [instruction, image],
+    image-only self attention, and a feed-forward per stream whose input is the first-norm base
+    modulated by (1 + scale_mlp) plus a shift (the second adaptive norm's gate slot).  The three
+    image adaptive norms share one RMS reduction of the image tokens (as do the two instruction
+    ones); every residual update is one biq_block_glue pass."""
+    joint_attn: DoubleStreamAttention
+    image_self_attn: GqaAttention
+    image_ffn: LuminaFeedForward
+    instruction_ffn: LuminaFeedForward
+    image_norm1: RmsNormZero
+    image_norm2: RmsNormZero
+    image_norm3: RmsNormZero
+    instruction_norm1: RmsNormZero
+    instruction_norm2: RmsNormZero
+    image_attn_norm: RmsNorm
+    image_self_norm: RmsNorm
+    image_ffn_norm1: RmsNorm
+    image_ffn_norm2: RmsNorm
+    instruction_attn_norm: RmsNorm
+    instruction_ffn_norm1: RmsNorm
+    instruction_ffn_norm2: RmsNorm
+    activation_dtype: torch.dtype = torch.float32
+
+    def forward(self, image: torch.Tensor, instruction: torch.Tensor,
+                image_rope: Tuple[torch.Tensor, torch.Tensor], joint_rope: Tuple[torch.Tensor, torch.Tensor],
+                conditioning: torch.Tensor):
+        for a, b in ((self.image_norm1, self.image_norm2), (self.image_norm1, self.image_norm3),
+                     (self.instruction_norm1, self.instruction_norm2)):
+            if a.norm.epsilon != b.norm.epsilon:
+                raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG,
+                                           "shared RMS normalization requires equal epsilons")
+        image = image.to(torch.float32).contiguous()
+        instruction = instruction.to(torch.float32).contiguous()
+        W = image.shape[-1]
+        adt = self.activation_dtype
+
+        def adaptive(norm: RmsNormZero, tokens: torch.Tensor, dtype: torch.dtype):
+            # forward_from_rms_normalized (norm.rs:138-152) on rms_normalized(tokens)
+            scale, g1, g2, g3 = (t.contiguous() for t in modulation_rows(norm.linear, conditioning, W, 4))
+            base = block_glue(tokens, next_norm=norm.norm, next_scale=scale, next_dtype=dtype)
+            return base, g1, g2, g3
+
+        img_joint, img_gate_attn, img_scale_mlp, img_gate_mlp = adaptive(self.image_norm1, image, adt)
+        img_mlp_base, img_shift_mlp, _, _ = adaptive(self.image_norm2, image, torch.float32)
+        img_self, img_gate_self, _, _ = adaptive(self.image_norm3, image, adt)
+        ins_joint, ins_gate_attn, ins_scale_mlp, ins_gate_mlp = adaptive(self.instruction_norm1, instruction, adt)
+        ins_mlp_base, ins_shift_mlp, _, _ = adaptive(self.instruction_norm2, instruction, torch.float32)
+
+        img_attn, ins_attn = self.joint_attn.forward(img_joint, ins_joint, joint_rope)
+        img_self_out = self.image_self_attn.forward(img_self, img_self, image_rope)
+
+        img1 = torch.empty_like(image)
+        block_glue(img_attn.contiguous(), residual=image, branch_norm=self.image_attn_norm,
+                   gate=img_gate_attn, residual_out=img1)
+        block_glue(img_self_out.contiguous(), residual=img1, branch_norm=self.image_self_norm,
+                   gate=img_gate_self, residual_out=img1)
+        img_ffn_in = block_glue(img_mlp_base, branch_scale=img_scale_mlp, branch_shift=img_shift_mlp,
+                                next_norm=self.image_ffn_norm1, next_dtype=adt)
+        img_mlp = self.image_ffn.forward(img_ffn_in).contiguous()
+        block_glue(img_mlp, residual=img1, branch_norm=self.image_ffn_norm2, gate=img_gate_mlp, residual_out=img1)
+
+        ins1 = torch.empty_like(instruction)
+        block_glue(ins_attn.contiguous(), residual=instruction, branch_norm=self.instruction_attn_norm,
+                   gate=ins_gate_attn, residual_out=ins1)
+        ins_ffn_in = block_glue(ins_mlp_base, branch_scale=ins_scale_mlp, branch_shift=ins_shift_mlp,
+                                next_norm=self.instruction_ffn_norm1, next_dtype=adt)
+        ins_mlp = self.instruction_ffn.forward(ins_ffn_in).contiguous()
+        block_glue(ins_mlp, residual=ins1, branch_norm=self.instruction_ffn_norm2, gate=ins_gate_mlp,
+                   residual_out=ins1)
+        return img1, ins1

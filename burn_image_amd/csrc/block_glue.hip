@@ -2,9 +2,12 @@
 // gfx950: strict-f32 RMS normalisation, tanh-gated residual update and (1 + scale) modulation,
 // fused so that each glue step reads and writes every activation row once.
 //
-//   r    = x + (branch / rms(branch)) * gamma_b * tanh(gate[b])       (x given: residual update)
-//   r    = branch                                                     (x NULL)
+//   u    = branch * (1 + branch_scale[b]) + branch_shift[b]          (either may be NULL)
+//   r    = x + (u / rms(u)) * gamma_b * tanh(gate[b])                 (x given: residual update)
+//   r    = u                                                          (x NULL)
 //   next = ((r / rms(r)) * gamma_n) * (1 + scale[b])                  (next_out given)
+// The branch modulation u is the dual-stream block's MLP input, base * (scale_mlp + 1) +
+// shift_mlp (block.rs:322-324,341-344).
 //
 // rms(v) = sqrt(mean(v^2) + eps) over the row, reduced in f32 (rms_normalized, norm.rs:28-35;
 // Burn's nn::RmsNorm for the gamma product; RmsNormZero's modulation order, norm.rs:144-152).
@@ -50,6 +53,7 @@ struct GlueArgs {
   const float *x;
   const void *branch;
   int branch_dtype;
+  const float *branch_scale, *branch_shift;
   const float *branch_gamma;
   float branch_eps;
   const float *gate;
@@ -67,20 +71,27 @@ __global__ void __launch_bounds__(GT) block_glue_kernel(GlueArgs a) {
   const int64_t b = row / a.rows_per_batch;
   const int64_t W = a.width, base = row * W;
   const float inv_w = 1.0f / (float)W;
+  // the (optionally modulated) branch element i of this row
+  auto branch_at = [&](int64_t i) {
+    float v = load_elem(a.branch, a.branch_dtype, base + i);
+    if (a.branch_scale) v *= a.branch_scale[b * W + i] + 1.0f;
+    if (a.branch_shift) v += a.branch_shift[b * W + i];
+    return v;
+  };
 
   // residual branch: r = x + branch / rms(branch) * gamma * tanh(gate), or r = branch
   float rms_b = 1.0f;
   if (a.x) {
     float ss = 0.0f;
     for (int64_t i = threadIdx.x; i < W; i += GT) {
-      const float v = load_elem(a.branch, a.branch_dtype, base + i);
+      const float v = branch_at(i);
       ss += v * v;
     }
     rms_b = sqrtf(block_sum(ss, red) * inv_w + a.branch_eps);
   }
   float ss_r = 0.0f;
   for (int64_t i = threadIdx.x; i < W; i += GT) {
-    const float v = load_elem(a.branch, a.branch_dtype, base + i);
+    const float v = branch_at(i);
     float r = v;
     if (a.x) {
       float nb = v / rms_b;
@@ -101,13 +112,13 @@ __global__ void __launch_bounds__(GT) block_glue_kernel(GlueArgs a) {
       if (a.x_out) {
         r = a.x_out[base + i];
       } else {
-        float nb = load_elem(a.branch, a.branch_dtype, base + i) / rms_b;
+        float nb = branch_at(i) / rms_b;
         if (a.branch_gamma) nb *= a.branch_gamma[i];
         if (a.gate) nb *= tanhf(a.gate[b * W + i]);
         r = a.x[base + i] + nb;
       }
     } else {
-      r = load_elem(a.branch, a.branch_dtype, base + i);
+      r = branch_at(i);
     }
     float n = r / rms_r;
     if (a.next_gamma) n *= a.next_gamma[i];
@@ -120,6 +131,7 @@ __global__ void __launch_bounds__(GT) block_glue_kernel(GlueArgs a) {
 
 extern "C" int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t rows_per_batch,
                               const float *x, const void *branch, int branch_dtype,
+                              const float *branch_scale, const float *branch_shift,
                               const float *branch_gamma, float branch_eps, const float *gate,
                               float *x_out, const float *next_gamma, float next_eps,
                               const float *next_scale, void *next_out, int next_dtype) {
@@ -135,9 +147,35 @@ extern "C" int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t
   if (x && !x_out && !next_out) return biq::fail(BIQ_ERR_INVALID_ARG, "block glue has nothing to write");
   if (!(branch_eps >= 0.0f) || !(next_eps >= 0.0f))
     return biq::fail(BIQ_ERR_INVALID_ARG, "block glue epsilons must be non-negative");
-  GlueArgs a{rows, width, rows_per_batch, x, branch, branch_dtype, branch_gamma, branch_eps, gate,
+  GlueArgs a{rows, width, rows_per_batch, x, branch, branch_dtype, branch_scale, branch_shift, branch_gamma, branch_eps, gate,
              x_out, next_gamma, next_eps, next_scale, next_out, next_dtype};
   hipLaunchKernelGGL(block_glue_kernel, dim3((unsigned)rows), dim3(GT), 0,
                      reinterpret_cast<hipStream_t>(stream), a);
   return biq::check_launch("block glue");
+}
+
+// ---------------------------------------------------------------------------------------------
+// silu of the conditioning rows before the modulation projection (RmsNormZero,
+// crates/burn_boogu/src/model/norm.rs:145: linear_forward(&self.linear, silu(conditioning))).
+// silu(a) = a / (1 + e^-a) in f32; output f32.
+// ---------------------------------------------------------------------------------------------
+namespace {
+__global__ void __launch_bounds__(256) silu_kernel(int64_t n, const void *x, int dt, float *y) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float a = load_elem(x, dt, i);
+  y[i] = a / (1.0f + expf(-a));
+}
+}  // namespace
+
+extern "C" int biq_silu(void *stream, int64_t n, const void *x, int x_dtype, float *y) {
+  biq::clear_error();
+  if (!x || !y) return biq::fail(BIQ_ERR_INVALID_ARG, "null pointer argument");
+  if (n <= 0) return biq::fail(BIQ_ERR_INVALID_ARG, "silu requires a non-empty input");
+  if (x_dtype != BIQ_DTYPE_F32 && x_dtype != BIQ_DTYPE_F16 && x_dtype != BIQ_DTYPE_BF16)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "silu input dtype must be F32, F16 or BF16");
+  if ((n + 255) / 256 > 0x7fffffffLL) return biq::fail(BIQ_ERR_UNSUPPORTED, "silu input too large");
+  hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), n, x, x_dtype, y);
+  return biq::check_launch("silu");
 }

@@ -124,21 +124,29 @@ int biq_q4_linear_swiglu(void *stream, const void *x, int x_dtype, int64_t M, in
                          const uint32_t *words3, const float *scales3, int layout, int block,
                          int64_t N, void *y, int y_dtype);
 
-/* Row-wise glue of the modulated DiT block (crates/burn_boogu/src/model/block.rs:91-111), one
- * pass per glue step over rows of `width` (b = row / rows_per_batch selects gate/scale rows):
- *   r    = x + (branch / rms(branch)) * branch_gamma * tanh(gate[b])   when x != NULL
- *   r    = branch                                                      when x == NULL
+/* Row-wise glue of the modulated DiT blocks (crates/burn_boogu/src/model/block.rs:91-111 and the
+ * dual-stream block, block.rs:248-350), one pass per glue step over rows of `width`
+ * (b = row / rows_per_batch selects the per-batch gate / scale / shift rows):
+ *   u    = branch * (1 + branch_scale[b]) + branch_shift[b]            (NULL: factor 1 / shift 0)
+ *   r    = x + (u / rms(u)) * branch_gamma * tanh(gate[b])             when x != NULL
+ *   r    = u                                                           when x == NULL
  *   x_out = r (f32; may alias x), when x_out != NULL
  *   next = ((r / rms(r)) * next_gamma) * (1 + next_scale[b]) in next_dtype, when next_out != NULL
  * rms(v) = sqrt(mean(v^2) + eps) in f32 (rms_normalized, crates/burn_boogu/src/model/norm.rs:
  * 28-35; nn::RmsNorm's gamma product; RmsNormZero's modulation, norm.rs:144-152).  A NULL gamma
  * is all ones, a NULL gate drops the tanh factor (the unmodulated block, block.rs:113-131) and a
- * NULL next_scale is all zeros.  branch may be F32, F16 or BF16; next_out must not alias x,
- * x_out or branch. */
+ * NULL next_scale is all zeros.  The branch modulation is the dual-stream block's MLP input,
+ * base * (scale_mlp + 1) + shift_mlp (block.rs:322-324).  branch may be F32, F16 or BF16;
+ * next_out must not alias x, x_out or branch. */
 int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t rows_per_batch,
-                   const float *x, const void *branch, int branch_dtype, const float *branch_gamma,
-                   float branch_eps, const float *gate, float *x_out, const float *next_gamma,
-                   float next_eps, const float *next_scale, void *next_out, int next_dtype);
+                   const float *x, const void *branch, int branch_dtype, const float *branch_scale,
+                   const float *branch_shift, const float *branch_gamma, float branch_eps,
+                   const float *gate, float *x_out, const float *next_gamma, float next_eps,
+                   const float *next_scale, void *next_out, int next_dtype);
+
+/* y[i] = silu(x[i]) = x / (1 + e^-x) in f32 for n elements: the conditioning rows entering
+ * RmsNormZero's modulation projection (crates/burn_boogu/src/model/norm.rs:145). */
+int biq_silu(void *stream, int64_t n, const void *x, int x_dtype, float *y);
 
 /* Key-mask modes of biq_attention (the byte mask is [B, Skv], one byte per key).
  * BIQ_KEY_MASK_VALID: a nonzero byte marks a key that may be attended (Qwen's `attention_mask`,
