@@ -7,9 +7,11 @@ from .attention import (F16_STORAGE_F32_ACCUM, STRICT_F32, AttentionKernel, burn
                         check_cu_seqlens, frame_ranges_to_cu_seqlens,
                         NativeQ4FlashAttention, RmsNorm, attention,
                         effective_portable_query_chunk_size, qk_norm_rope)
-from .block import GqaAttention, RmsNormZero, SingleStreamBlock, block_glue
+from .block import (DoubleStreamAttention, DoubleStreamBlock, GqaAttention, RmsNormZero,
+                    SingleStreamBlock, block_glue)
 from .linear import (Linear, LuminaFeedForward, linear_forward, q_matmul, q_matmul_swiglu,
                      qwen_linear_forward)
+from .qwen import Qwen3VlTextAttention
 from .q4 import (BOOGU_DENOISER, FLUX_VAE, QWEN3_VL, Q4Weight, from_packed,
                  q4s_storage_block_and_axis, q4s_stored_dtype, quantize_q4s_block128_f32,
                  quantize_row_layout_q4s_block_up_to128_f32)
@@ -25,6 +27,7 @@ __all__ = [
     "qwen_linear_forward", "Q4Weight", "from_packed",
     "q4s_storage_block_and_axis", "q4s_stored_dtype", "quantize_q4s_block128_f32",
     "quantize_row_layout_q4s_block_up_to128_f32", "BiqError", "InvalidArgument", "Unsupported",
-    "block_glue", "RmsNormZero", "GqaAttention", "SingleStreamBlock",
+    "block_glue", "RmsNormZero", "GqaAttention", "SingleStreamBlock", "DoubleStreamAttention",
+    "DoubleStreamBlock", "Qwen3VlTextAttention",
     "version", "BOOGU_DENOISER", "QWEN3_VL", "FLUX_VAE", "Q4_KN_AXIS1", "Q4_NK_AXIS0",
 ]

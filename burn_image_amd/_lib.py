@@ -22,6 +22,9 @@ DTYPE_F32 = 0
 DTYPE_F16 = 1
 DTYPE_BF16 = 2
 
+ROPE_INTERLEAVED = 0  # Boogu pairs (2p, 2p + 1)
+ROPE_HALF = 1         # Qwen rotate_half pairs (i, i + D/2)
+
 KEY_MASK_VALID = 0            # nonzero byte = key may be attended (Qwen attention_mask)
 KEY_MASK_VALID_FILL_MEAN = 1  # as VALID; rows with no visible key = mean of V (Qwen -1e30 fill)
 KEY_MASK_MASKED = 2           # nonzero byte = key masked out (Burn bool mask polarity)
@@ -57,7 +60,7 @@ SIGNATURES = {
     "biq_frame_ranges_to_cu_seqlens": ([_P, _I64, _I64, _P], _I),
     "biq_qk_norm_rope": ([_P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _I64,
                           ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I64),
-                          _P, _P, ctypes.c_float, ctypes.c_float, _P, _P, _I64, _I, _P, _P, _P], _I),
+                          _P, _P, ctypes.c_float, ctypes.c_float, _P, _P, _I64, _I, _I, _P, _P, _P], _I),
 }
 
 _lib = None

@@ -233,10 +233,13 @@ class RmsNorm:
 
 def qk_norm_rope(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, norm_q: RmsNorm,
                  norm_k: RmsNorm, cos: torch.Tensor, sin: torch.Tensor,
-                 out_dtype: torch.dtype = torch.float16, stream: Optional[int] = None):
-    """One fused HIP pass over token-major Q [B, S, Hq, D], K/V [B, S, Hkv, D]: strict-F32
-    RMSNorm + interleaved RoPE on Q and K, cast of all three to ``out_dtype``
-    (native_flash.rs:395-583).  cos/sin: [1 or B, S, D].  Returns contiguous (q, k, v)."""
+                 out_dtype: torch.dtype = torch.float16, rope_layout: int = _lib.ROPE_INTERLEAVED,
+                 stream: Optional[int] = None):
+    """One fused HIP pass over token-major Q [B, S, Hq, D], K/V [B, S, Hkv, D]: RMSNorm (f32
+    reduction, then in the input dtype) + RoPE on Q and K, cast of all three to ``out_dtype``.
+    ROPE_INTERLEAVED: Boogu's fused prep (native_flash.rs:395-583); ROPE_HALF: Qwen's q/k norm +
+    apply_text_rope (text.rs:112-125,407-440).  cos/sin: [1 or B, S, D].  Returns contiguous
+    (q, k, v)."""
     B, S, Hq, D = query.shape
     _, Sk, Hkv, _ = key.shape
     if Sk != S or value.shape[1] != S:
@@ -263,7 +266,7 @@ def qk_norm_rope(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, no
     _lib.check(_lib.load().biq_qk_norm_rope(
         s, query.data_ptr(), key.data_ptr(), value.data_ptr(), _DTYPE_CODE[query.dtype],
         B, S, Hq, Hkv, D, st(query), st(key), st(value), gq.data_ptr(), gk.data_ptr(),
-        norm_q.epsilon, norm_k.epsilon, cs.data_ptr(), sn.data_ptr(), cs.shape[0],
+        norm_q.epsilon, norm_k.epsilon, cs.data_ptr(), sn.data_ptr(), cs.shape[0], int(rope_layout),
         _DTYPE_CODE[out_dtype], qo.data_ptr(), ko.data_ptr(), vo.data_ptr()))
     return qo, ko, vo
 

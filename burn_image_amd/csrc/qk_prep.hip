@@ -1,18 +1,29 @@
-// Fused Q/K preparation before attention for gfx950: strict-F32 RMSNorm, Boogu interleaved-pair
-// RoPE and the cast to the attention operand type, plus the V cast, in one HBM pass.
+// Fused Q/K preparation before attention for gfx950: strict RMSNorm, RoPE and the cast to the
+// attention operand type, plus the V cast, in one HBM pass.
 //
 // Restates prepare_gqa_strict_norm_rope_padded_qkv_kernel (crates/burn_boogu/src/model/
 // native_flash.rs:395-583; host side :2205-2332) for a kernel that consumes the unpadded head
 // width and unexpanded KV heads directly: no 120 -> 128 zero padding, no sqrt(128/120) Q prescale
 // and no GQA head copies are written (the attention kernel indexes KV heads and masks the width).
+// The rotate-half layout restates Qwen's q_norm / k_norm (Burn nn::RmsNorm) followed by
+// apply_text_rope (crates/burn_qwen3_vl/src/text.rs:112-125,407-440).
 //
-// Per row (one wave; lane p owns the pair d = 2p, 2p + 1):
-//   rms = sqrt(sum_d x_d^2 / D + eps)            f32 (x widened to f32)
-//   n_d = x_d / rms * gamma_d                    f32
-//   y_2p   = n_2p * cos_2p - n_2p+1 * sin_2p     f32 (rotated = (-x1, x0), attention.rs:916-928)
-//   y_2p+1 = n_2p+1 * cos_2p+1 + n_2p * sin_2p+1
-//   out_d = cast(y_d)                            f16 or bf16 (round to nearest even)
+// Per row (one wave; lane p owns the elements d = 2p, 2p + 1), F = the input type, rnd = rounding
+// to F (identity for F32 inputs):
+//   rms   = sqrt(sum_d x_d^2 / D + eps)                  f32 (x widened to f32)
+//   n_d   = rnd(rnd(x_d / rnd(rms)) * rnd(gamma_d))      in F: the f32 rms is cast to F first
+//                                                        (native_flash.rs:446-449; norm.rs:28-35)
+//   interleaved pairs (Boogu, attention.rs:916-928), rotated = (-n_2p+1, n_2p), in F:
+//     y_d = rnd(rnd(n_d * rnd(cos_d)) + rnd(rot_d * rnd(sin_d)))
+//   rotate-half (Qwen), rotated = cat(-n[h:], n[:h]), in f32 then cast to F:
+//     y_d = rnd(n_d * cos_d + rot_d * sin_d)
+//   out_d = cast(y_d)                                    f16 or bf16 (round to nearest even)
+// Products of two 16-bit values and sums of two are exact in f32, so each f32 operation rounded
+// to F is F's own rounded operation; the division may differ from a correctly rounded F division
+// by one unit of F in rare midpoint cases.  Contraction into FMA is off for these steps.
 #include <math.h>
+
+#include <type_traits>
 
 #include "common.h"
 
@@ -27,6 +38,18 @@ struct PrepArgs {
   int64_t B, S, Hq, Hkv, D;
   void *qo, *ko, *vo;  // contiguous [B, S, H, D]
 };
+
+// Round an f32 value to the input type InT, returned as f32.
+template <typename InT>
+__device__ __forceinline__ float rnd(float v) {
+  if constexpr (sizeof(InT) == 4) {
+    return v;
+  } else if constexpr (std::is_same<InT, f16_t>::value) {
+    return (float)(_Float16)v;
+  } else {
+    return biq::bitcast<float>(biq::f32_to_bf16_bits(v) << 16);
+  }
+}
 
 template <typename T>
 __device__ __forceinline__ float2 load_pair(const T *p);
@@ -56,8 +79,9 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-template <typename InT>
+template <typename InT, bool HALF>
 __global__ void __launch_bounds__(256) qk_prep_kernel(PrepArgs p, int out_bf16) {
+#pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t q_rows = p.B * p.S * p.Hq, kv_rows = p.B * p.S * p.Hkv;
@@ -85,15 +109,28 @@ __global__ void __launch_bounds__(256) qk_prep_kernel(PrepArgs p, int out_bf16) 
   }
   const float sum_sq = wave_sum(x.x * x.x + x.y * x.y);  // wave-uniform
   const float eps = kind == 0 ? p.q_eps : p.k_eps;
-  const float rms = sqrtf(sum_sq / (float)p.D + eps);
-  if (!active) return;
+  const float rms = rnd<InT>(sqrtf(sum_sq / (float)p.D + eps));
   const float *g = kind == 0 ? p.q_gamma : p.k_gamma;
-  const float n0 = x.x / rms * g[d];
-  const float n1 = x.y / rms * g[d + 1];
+  const float n0 = active ? rnd<InT>(rnd<InT>(x.x / rms) * rnd<InT>(g[d])) : 0.0f;
+  const float n1 = active ? rnd<InT>(rnd<InT>(x.y / rms) * rnd<InT>(g[d + 1])) : 0.0f;
   const float *cs = p.cos + b * p.rope_bs + s * p.D;
   const float *sn = p.sin + b * p.rope_bs + s * p.D;
-  const float y0 = n0 * cs[d] + (-n1) * sn[d];
-  const float y1 = n1 * cs[d + 1] + n0 * sn[d + 1];
+  float y0, y1;
+  if constexpr (HALF) {
+    // partner elements d + h (first half) or d - h (second half) sit in lane p +- h / 2; every
+    // lane takes part in the shuffles (D % 4 == 0, host check)
+    const int hp = (int)(p.D / 4);
+    const int src = d < 2 * hp ? lane + hp : lane - hp;
+    const float m0 = __shfl(n0, src), m1 = __shfl(n1, src);
+    if (!active) return;
+    const float r0 = d < 2 * hp ? -m0 : m0, r1 = d < 2 * hp ? -m1 : m1;
+    y0 = rnd<InT>(n0 * cs[d] + r0 * sn[d]);
+    y1 = rnd<InT>(n1 * cs[d + 1] + r1 * sn[d + 1]);
+  } else {
+    if (!active) return;
+    y0 = rnd<InT>(rnd<InT>(n0 * rnd<InT>(cs[d])) + rnd<InT>(-n1 * rnd<InT>(sn[d])));
+    y1 = rnd<InT>(rnd<InT>(n1 * rnd<InT>(cs[d + 1])) + rnd<InT>(n0 * rnd<InT>(sn[d + 1])));
+  }
   *reinterpret_cast<uint32_t *>(dst + d) = store_bits(y0, y1, out_bf16);
 }
 
@@ -104,8 +141,8 @@ extern "C" int biq_qk_norm_rope(void *stream, const void *q, const void *k, cons
                                 int64_t D, const int64_t *q_strides, const int64_t *k_strides,
                                 const int64_t *v_strides, const float *q_gamma,
                                 const float *k_gamma, float q_eps, float k_eps, const float *cos,
-                                const float *sin, int64_t rope_batch, int out_dtype, void *q_out,
-                                void *k_out, void *v_out) {
+                                const float *sin, int64_t rope_batch, int rope_layout,
+                                int out_dtype, void *q_out, void *k_out, void *v_out) {
   biq::clear_error();
   if (!q || !k || !v || !q_gamma || !k_gamma || !cos || !sin || !q_out || !k_out || !v_out ||
       !q_strides || !k_strides || !v_strides)
@@ -120,6 +157,10 @@ extern "C" int biq_qk_norm_rope(void *stream, const void *q, const void *k, cons
     return biq::fail(BIQ_ERR_INVALID_ARG, "GQA query heads must be divisible by key/value heads");
   if (D <= 0 || D > 128 || D % 2 != 0)
     return biq::fail(BIQ_ERR_UNSUPPORTED, "fused preparation head width must be even and at most 128");
+  if (rope_layout != BIQ_ROPE_INTERLEAVED && rope_layout != BIQ_ROPE_HALF)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "unknown RoPE layout");
+  if (rope_layout == BIQ_ROPE_HALF && D % 4 != 0)
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "rotate-half RoPE needs a head width divisible by 4");
   if (rope_batch != 1 && rope_batch != B)
     return biq::fail(BIQ_ERR_INVALID_ARG, "fused RoPE batch must be one or match Q/K batch");
   if (!(q_eps > 0.0f) || !(k_eps > 0.0f) || q_eps == INFINITY || k_eps == INFINITY)
@@ -147,11 +188,17 @@ extern "C" int biq_qk_norm_rope(void *stream, const void *q, const void *k, cons
   if (blocks > 0x7fffffff) return biq::fail(BIQ_ERR_UNSUPPORTED, "fused preparation grid too large");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int ob = out_dtype == BIQ_DTYPE_BF16;
-  if (in_dtype == BIQ_DTYPE_F32)
-    hipLaunchKernelGGL(qk_prep_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, s, a, ob);
-  else if (in_dtype == BIQ_DTYPE_F16)
-    hipLaunchKernelGGL(qk_prep_kernel<f16_t>, dim3((unsigned)blocks), dim3(256), 0, s, a, ob);
-  else
-    hipLaunchKernelGGL(qk_prep_kernel<bf16_t>, dim3((unsigned)blocks), dim3(256), 0, s, a, ob);
+  const dim3 grid((unsigned)blocks);
+#define BIQ_PREP(T)                                                                      \
+  do {                                                                                   \
+    if (rope_layout == BIQ_ROPE_HALF)                                                    \
+      hipLaunchKernelGGL((qk_prep_kernel<T, true>), grid, dim3(256), 0, s, a, ob);       \
+    else                                                                                 \
+      hipLaunchKernelGGL((qk_prep_kernel<T, false>), grid, dim3(256), 0, s, a, ob);      \
+  } while (0)
+  if (in_dtype == BIQ_DTYPE_F32) BIQ_PREP(float);
+  else if (in_dtype == BIQ_DTYPE_F16) BIQ_PREP(f16_t);
+  else BIQ_PREP(bf16_t);
+#undef BIQ_PREP
   return biq::check_launch("qk norm rope");
 }

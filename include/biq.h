@@ -221,26 +221,37 @@ int biq_check_cu_seqlens(const int32_t *cu, int64_t nseg, int64_t S);
  * (the reference's per-frame loop concatenates the frame outputs in order). */
 int biq_frame_ranges_to_cu_seqlens(const int64_t *ranges, int64_t nframes, int64_t S, int32_t *cu);
 
-/* Fused attention-input preparation: strict-F32 RMSNorm of Q and K rows, Boogu interleaved-pair
- * RoPE on both, and the cast of Q, K and V to the attention operand type, in one pass.
- * Replaces prepare_gqa_strict_norm_rope_padded_qkv_kernel and its host function
- * (crates/burn_boogu/src/model/native_flash.rs:395-583,747-817,2205-2332; the
- * FusedStrictF32ToF16 policy of crates/burn_boogu/src/config.rs:177-192) for an attention
- * kernel that takes the unpadded head width and unexpanded KV heads: it writes no 120 -> 128
- * padding, no sqrt(128/120) Q prescale and no GQA copies.
+/* RoPE layouts of biq_qk_norm_rope: Boogu's interleaved pairs (2p, 2p + 1), rotated = (-x1, x0)
+ * (crates/burn_boogu/src/model/attention.rs:916-928), and Qwen's rotate-half pairs (i, i + D/2),
+ * rotated = cat(-x[D/2:], x[:D/2]) (crates/burn_qwen3_vl/src/text.rs:407-440). */
+#define BIQ_ROPE_INTERLEAVED 0
+#define BIQ_ROPE_HALF 1
+
+/* Fused attention-input preparation: RMSNorm of Q and K rows, RoPE on both, and the cast of Q,
+ * K and V to the attention operand type, in one pass.
+ * With BIQ_ROPE_INTERLEAVED it replaces prepare_gqa_strict_norm_rope_padded_qkv_kernel and its
+ * host function (crates/burn_boogu/src/model/native_flash.rs:395-583,747-817,2205-2332; the
+ * FusedStrictF32ToF16 policy of crates/burn_boogu/src/config.rs:177-192) for an attention kernel
+ * that takes the unpadded head width and unexpanded KV heads: it writes no 120 -> 128 padding,
+ * no sqrt(128/120) Q prescale and no GQA copies.  With BIQ_ROPE_HALF it is Qwen's q_norm / k_norm
+ * (Burn nn::RmsNorm) followed by apply_text_rope (crates/burn_qwen3_vl/src/text.rs:112-125,
+ * 407-440).
  *   q: [B, S, Hq, D], k, v: [B, S, Hkv, D] token-major, addressed by {batch, seq, head} element
- *   strides (D contiguous), in_dtype in {F32, F16, BF16};
+ *   strides (D contiguous), in_dtype F in {F32, F16, BF16};
  *   q_gamma, k_gamma: f32 [D]; cos, sin: f32 [rope_batch, S, D] contiguous, rope_batch 1 or B;
  *   q_out, k_out, v_out: contiguous [B, S, H, D] of out_dtype in {F16, BF16}.
- * Per row: rms = sqrt(sum(x^2) / D + eps) in f32, n = x / rms * gamma, rotated pairs
- * (-n1, n0), y = n * cos + rotated * sin in f32, then one rounding to out_dtype.
- * D even and at most 128; eps finite and positive; Hq % Hkv == 0. */
+ * Per row: rms = sqrt(sum(x^2) / D + eps) in f32, cast to F; n = x / rms * gamma in F (gamma
+ * cast to F); interleaved: y = n * cos + rotated * sin in F (tables cast to F), rotate-half: in
+ * f32 then cast to F; then one rounding to out_dtype.  For F32 inputs every step is f32.
+ * D even and at most 128 (divisible by 4 for BIQ_ROPE_HALF); eps finite and positive;
+ * Hq % Hkv == 0. */
 int biq_qk_norm_rope(void *stream, const void *q, const void *k, const void *v, int in_dtype,
                      int64_t B, int64_t S, int64_t Hq, int64_t Hkv, int64_t D,
                      const int64_t *q_strides, const int64_t *k_strides,
                      const int64_t *v_strides, const float *q_gamma, const float *k_gamma,
                      float q_eps, float k_eps, const float *cos, const float *sin,
-                     int64_t rope_batch, int out_dtype, void *q_out, void *k_out, void *v_out);
+                     int64_t rope_batch, int rope_layout, int out_dtype, void *q_out, void *k_out,
+                     void *v_out);
 
 #ifdef __cplusplus
 }

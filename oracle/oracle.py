@@ -256,6 +256,45 @@ def apply_rope_half(x, cs, sn):
     return y
 
 
+def round_to(x, dtype: str) -> np.ndarray:
+    """Round float32 values to `dtype` ("f32", "f16", "bf16", nearest even), returned as f32."""
+    x = np.asarray(x, np.float32)
+    if dtype == "f32":
+        return x.copy()
+    if dtype == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    u = np.ascontiguousarray(x).view(np.uint32)
+    r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    return r.view(np.float32)
+
+
+def qk_norm_rope_ref(x, gamma, eps: float, cos, sin, in_dtype: str, layout: str):
+    """Per-row Q/K preparation before the final cast (rows [..., D], values representable in
+    in_dtype F).  The strict-F32 RMS is cast to F and the normalisation runs in F
+    (crates/burn_boogu/src/model/native_flash.rs:431-451: `let rms = F::cast_from(rms)`, then
+    `x / rms * gamma`; Burn's nn::RmsNorm via rms_normalized, norm.rs:28-35).  RoPE:
+    "interleaved" = the Boogu fused kernel's pairs in F (native_flash.rs:452-474, tables of type
+    F); "half" = Qwen's apply_text_rope in f32 then cast to F (crates/burn_qwen3_vl/src/
+    text.rs:425-440).  Each F operation is one f32 operation rounded to F."""
+    F = lambda a: round_to(a, in_dtype)  # noqa: E731
+    x = np.asarray(x, np.float32)
+    D = x.shape[-1]
+    ss = np.sum(x.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    rms = F(np.sqrt((ss.astype(np.float32) / np.float32(D)) + np.float32(eps)).astype(np.float32))
+    n = F(F(x / rms) * F(np.broadcast_to(np.asarray(gamma, np.float32), x.shape)))
+    cos = np.broadcast_to(np.asarray(cos, np.float32), x.shape)
+    sin = np.broadcast_to(np.asarray(sin, np.float32), x.shape)
+    rot = np.empty_like(n)
+    if layout == "interleaved":
+        rot[..., 0::2] = -n[..., 1::2]
+        rot[..., 1::2] = n[..., 0::2]
+        return F(F(n * F(cos)) + F(rot * F(sin)))
+    h = D // 2
+    rot[..., :h] = -n[..., h:]
+    rot[..., h:] = n[..., :h]
+    return F((n * cos).astype(np.float32) + (rot * sin).astype(np.float32))
+
+
 # ----------------------------------------------------------------------------------------------
 # Independent numpy restatements (cross-checks for the C oracle on small inputs)
 # ----------------------------------------------------------------------------------------------

@@ -287,3 +287,49 @@ def test_gpu_segment_masks_dtypes_widths_batches(gpu, oracle, dtype, D, causal):
     out = B.attention(qd, kd, vd, is_causal=causal, cu_seqlens=cu, out_dtype=torch.float32)
     ref = oracle.attention_f64(q, k, v, causal=causal, cu_seqlens=cu).astype(np.float32)
     assert_parity(host(out), ref, f"segment_{dtype}_D{D}_causal{int(causal)}")
+
+
+# ---------------------------------------------------------------------------------------------
+# fused Q/K preparation: 16-bit inputs (rms cast to the input dtype), bf16 outputs, rotate-half
+# ---------------------------------------------------------------------------------------------
+
+def _ulp(a, dt):
+    """Spacing of the output dtype at |a| (f16: 11-bit significand, bf16: 8-bit)."""
+    bits = 11 if dt == torch.float16 else 8
+    e = np.floor(np.log2(np.maximum(np.abs(a), 2.0 ** -14)))
+    return 2.0 ** (e - (bits - 1))
+
+
+@pytest.mark.parametrize("in_dt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("out_dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("layout", ["interleaved", "half"])
+def test_gpu_qk_prep_dtypes_and_layouts(gpu, oracle, in_dt, out_dt, layout):
+    """Every input dtype (F32, F16, BF16) x output dtype (F16, BF16) x RoPE layout (Boogu pairs,
+    Qwen rotate-half) against the oracle's restatement (the rms cast to the input dtype before the
+    division, native_flash.rs:446-449), within one unit of the output dtype: the oracle rounds
+    each step the same way; a division at a midpoint of F can land one unit apart."""
+    rng = np.random.default_rng(80 + len(in_dt) + (7 if out_dt == torch.bfloat16 else 0))
+    Bn, S, Hq, Hkv, D = 2, 33, 4, 2, 128
+    tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[in_dt]
+    q, k, v = (oracle.round_to(rng.standard_normal((Bn, S, h, D)).astype(np.float32) * 2.5, in_dt)
+               for h in (Hq, Hkv, Hkv))
+    gq = (1 + 0.25 * rng.standard_normal(D)).astype(np.float32)
+    gk = (1 + 0.25 * rng.standard_normal(D)).astype(np.float32)
+    ang = rng.uniform(0, 6.3, (Bn, S, D // 2))
+    rep = (lambda a: np.repeat(a, 2, axis=-1)) if layout == "interleaved" else (lambda a: np.concatenate([a, a], -1))
+    cos, sin = rep(np.cos(ang)).astype(np.float32), rep(np.sin(ang)).astype(np.float32)
+    lay = B._lib.ROPE_INTERLEAVED if layout == "interleaved" else B._lib.ROPE_HALF
+    qo, ko, vo = B.qk_norm_rope(dev(q, tdt, gpu), dev(k, tdt, gpu), dev(v, tdt, gpu),
+                                B.RmsNorm(dev(gq, device=gpu), 1e-5), B.RmsNorm(dev(gk, device=gpu), 1e-6),
+                                dev(cos, device=gpu), dev(sin, device=gpu), out_dtype=out_dt, rope_layout=lay)
+    assert qo.dtype == out_dt
+    odt = "f16" if out_dt == torch.float16 else "bf16"
+    for name, x, g, eps, out in (("q", q, gq, 1e-5, qo), ("k", k, gk, 1e-6, ko)):
+        cs = np.broadcast_to(cos[:, :, None, :], x.shape)
+        sn = np.broadcast_to(sin[:, :, None, :], x.shape)
+        exp = oracle.round_to(oracle.qk_norm_rope_ref(x, g, eps, cs, sn, in_dt, layout), odt)
+        got = host(out)
+        bad = np.abs(got - exp) > _ulp(exp, out_dt) * 1.0001
+        assert not bad.any(), f"{name}: {bad.sum()} elements beyond one unit, max {np.max(np.abs(got - exp))}"
+        assert np.mean(got == exp) > 0.99
+    assert np.array_equal(host(vo), oracle.round_to(v, odt))

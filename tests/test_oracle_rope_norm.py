@@ -83,3 +83,39 @@ def test_strict_rms_norm_reference(oracle):
     y2 = oracle.rms_norm(x * np.float32(4.0), gamma, 0.0)
     y1 = oracle.rms_norm(x, gamma, 0.0)
     assert np.max(np.abs(y2 - y1)) <= 2e-6
+
+
+def test_qk_prep_oracle_f32_reduces_to_pinned_norm_and_rope(oracle):
+    """For F32 inputs the fused preparation is the pinned strict RMSNorm followed by the pinned
+    RoPE restatements (interleaved pairs and rotate-half)."""
+    rng = np.random.default_rng(70)
+    x = rng.standard_normal((9, 64)).astype(np.float32) * 3
+    g = (1 + 0.1 * rng.standard_normal(64)).astype(np.float32)
+    cs = np.cos(rng.uniform(0, 6, (9, 64))).astype(np.float32)
+    sn = np.sin(rng.uniform(0, 6, (9, 64))).astype(np.float32)
+    n = oracle.rms_norm(x, g, 1e-5)
+    for layout, rope in (("interleaved", oracle.apply_rope_interleaved), ("half", oracle.apply_rope_half)):
+        y = oracle.qk_norm_rope_ref(x, g, 1e-5, cs, sn, "f32", layout)
+        assert np.max(np.abs(y - rope(n, cs, sn))) <= 4e-6 * np.max(np.abs(y))
+
+
+def test_qk_prep_oracle_16bit_rms_cast_to_input_dtype(oracle):
+    """native_flash.rs:446-449 casts the strict-F32 rms to the input dtype F before dividing: with
+    gamma = 1, cos = 1, sin = 0 the output is round_F(x / round_F(rms)), checked against exact
+    rational division; dividing by the unrounded f32 rms instead (a plausible mistake) differs."""
+    from fractions import Fraction
+    rng = np.random.default_rng(71)
+    for dt, npdt in (("f16", np.float16), ("bf16", None)):
+        x = oracle.round_to(rng.standard_normal((6, 32)).astype(np.float32) * 5, dt)
+        ones, zeros = np.ones((6, 32), np.float32), np.zeros((6, 32), np.float32)
+        y = oracle.qk_norm_rope_ref(x, np.ones(32, np.float32), 1e-6, ones, zeros, dt, "interleaved")
+        wrong = 0
+        for r in range(6):
+            rms32 = np.float32(np.sqrt(np.float32(np.sum(x[r].astype(np.float64) ** 2)) / np.float32(32) + np.float32(1e-6)))
+            rms_f = oracle.round_to(np.array([rms32]), dt)[0]
+            for d in range(32):
+                exact = Fraction(float(x[r, d])) / Fraction(float(rms_f))
+                want = oracle.round_to(np.array([float(exact)], np.float32), dt)[0]
+                assert y[r, d] == want, (dt, r, d)
+                wrong += oracle.round_to(np.array([np.float32(x[r, d]) / rms32]), dt)[0] != want
+        assert wrong > 0, dt  # the f32-rms variant is distinguishable on these rows
