@@ -4,10 +4,16 @@ One step = one pass of the hot path at the 4608-token Boogu Turbo shape over res
 inputs: the four packed-Q4 projection GEMMs (M 4608; K x N = 3072x9216 QKV, 3072x3072 O,
 3072x12288 MLP up, 12288x3072 MLP down; bf16 activations, f32 outputs) and the joint flash
 attention (B1 H24 S4608 D128, bf16 Q/K/V, f32 output).  Prints one JSON line.  After the timed
-steps it also times the fused SwiGLU projection (both 3072x12288 up weights in one pass) and
-reports the denoise block with it (`ms_per_denoise_block_fused_swiglu`).
+steps it also times, as extra keys:
+  * the fused SwiGLU projection (both 3072x12288 up weights in one pass);
+  * the whole modulated denoise block (SingleStreamBlock.forward: modulation GEMV, three glue
+    passes, fused QKV projection, Q/K norm + RoPE, attention, O, fused SwiGLU, down) at
+    4608 tokens x hidden 3072, 24 heads of 128, SwiGLU 12288, bf16 activations
+    (`ms_per_denoise_block`), next to the sum of its GEMM and attention kernels;
+  * the small-M route (one modulation row, 1 x 3072 x 12288, and 16 x 3072 x 9216) in GB/s over
+    >= 1 GB of rotating weights, replayed from a HIP graph.
 
-    python bench.py [--steps 20] [--warmup 3] [--no-cpu]
+    python bench.py [--steps 20] [--warmup 3] [--no-cpu] [--cpu-runs 5]
 """
 from __future__ import annotations
 
@@ -62,6 +68,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=4608,
                     help="query rows / activation rows of the CPU sample (4608 = the whole step)")
+    ap.add_argument("--cpu-runs", type=int, default=5,
+                    help="timed CPU runs per op after one warm-up run (the median is reported)")
     return ap.parse_args()
 
 
@@ -74,40 +82,140 @@ def cpu_baseline(args, words_np, scales_np, x_np, q_np, k_np, v_np):
     from oracle import oracle as O
     O.build()
     rows = args.cpu_rows
+    runs = max(1, args.cpu_runs)
     t_total = 0.0
     threads = 1
     detail = {}
+
+    def median_time(fn):
+        fn()  # warm-up (page-in, thread pool start)
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
     for (name, K, N) in GEMMS:
         xs = np.ascontiguousarray(x_np[name][:rows])
-        t0 = time.perf_counter()
-        _, threads = O.cpu_q4_linear_f32(xs, words_np[name], scales_np[name], 1, 128, N)
-        dt = time.perf_counter() - t0
+        box = {}
+        dt = median_time(lambda: box.update(t=O.cpu_q4_linear_f32(xs, words_np[name], scales_np[name], 1, 128, N)[1]))
+        threads = box["t"]
         rate = gemm_flops(rows, K, N) / dt
         detail[name] = rate / 1e12
         t_total += gemm_flops(M_TOKENS, K, N) / rate
-    t0 = time.perf_counter()
-    O.cpu_attention_f32(q_np, k_np, v_np, requested_chunk=8192, q_rows=rows)
-    dt = time.perf_counter() - t0
+    dt = median_time(lambda: O.cpu_attention_f32(q_np, k_np, v_np, requested_chunk=8192, q_rows=rows))
     rate = (4.0 * ATTN["H"] * ATTN["D"] * rows * ATTN["S"]) / dt
     detail["attention"] = rate / 1e12
     t_total += attn_flops(**ATTN) / rate
     step_flops = sum(gemm_flops(M_TOKENS, K, N) for _, K, N in GEMMS) + attn_flops(**ATTN)
     if rows >= M_TOKENS:
         scope = ("the whole step: all 4608 rows of each Q4 GEMM and all 4608 query rows x 24 heads "
-                 "of the attention, each op timed once")
+                 "of the attention")
     else:
         scope = (f"the first {rows} of 4608 rows of each Q4 GEMM and {rows} query rows x 24 heads "
                  f"of the attention; per-op rates extrapolated to one full step")
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     return {
         "value": step_flops / t_total / 1e12,
         "unit": "TFLOP/s",
         "cores": int(threads),
         "kind": "port",
         "sample": ("restated Burn NdArray CPU path (dequantise + f32 matmul; query-chunked f32 "
-                   "attention, chunk policy of attention.rs:36-45) on " + scope),
+                   "attention, chunk policy of attention.rs:36-45) on " + scope +
+                   f"; median of {runs} runs per op after one warm-up"),
+        "cpu_model": cpu_model,
+        "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+        "nproc": os.cpu_count(),
         "per_op_tflops": {k: round(v, 5) for k, v in detail.items()},
         "ms_per_step": t_total * 1e3,
     }
+
+
+def time_denoise_block(B, W, dev, weights, w3, args):
+    """SingleStreamBlock.forward (block.rs:84-134) at 4608 x 3072: modulation GEMV, three glue
+    passes, fused QKV, Q/K norm + RoPE, attention, O, fused SwiGLU, down; bf16 activations.
+    Returns the mean ms per forward (events around each call)."""
+    import torch
+    from burn_image_amd import block as BL
+    from burn_image_amd import rope as R
+    Wd, H, D, C = 3072, 24, 128, 1024
+    ones = lambda n: torch.ones(n, device=dev)  # noqa: E731
+    wm, sm = W.q4_weight(3, 11, C, 4 * Wd, layout=1)
+    mod = B.from_packed(torch.from_numpy(wm.view(np.int32)).to(dev), torch.from_numpy(sm).to(dev), 1, 128, (C, 4 * Wd))
+    attn = BL.GqaAttention(None, None, None, B.Linear(weights["o"]), B.RmsNorm(ones(D)), B.RmsNorm(ones(D)),
+                           H, H, D, qkv=B.Linear(weights["qkv"]))
+    blk = BL.SingleStreamBlock(
+        norm1=BL.RmsNormZero(B.Linear(mod, torch.zeros(4 * Wd, device=dev)), B.RmsNorm(ones(Wd))),
+        attn=attn, norm2=B.RmsNorm(ones(Wd)), ffn_norm1=B.RmsNorm(ones(Wd)), ffn_norm2=B.RmsNorm(ones(Wd)),
+        feed_forward=B.LuminaFeedForward(B.Linear(weights["mlp_up"]), B.Linear(weights["mlp_down"]), B.Linear(w3)),
+        activation_dtype=torch.bfloat16)
+    ids = W.boogu_joint_ids(2)
+    cos, sin = R.rope_values(ids, [32, 48, 48], 1.0e4)
+    rope = (torch.from_numpy(cos[None]).to(dev), torch.from_numpy(sin[None]).to(dev))
+    gen = torch.Generator(device=dev).manual_seed(7)
+    tokens = torch.randn((1, M_TOKENS, Wd), device=dev, generator=gen)
+    cond = torch.randn((1, C), device=dev, generator=gen)
+    for _ in range(args.warmup):
+        blk.forward(tokens, rope, cond)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for e0, e1 in evs:
+        e0.record(stream)
+        blk.forward(tokens, rope, cond)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return float(np.mean([e0.elapsed_time(e1) for e0, e1 in evs]))
+
+
+def time_small_m(B, dev):
+    """The small-M route at the modulation row (1 x 3072 x 12288, f32 activations) and at
+    16 x 3072 x 9216 (bf16 activations), each over >= 1 GB of distinct weights (the 256 MB MALL
+    cannot hold them), replayed from a HIP graph; GB/s = algorithmic bytes / time."""
+    import torch
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(11)
+    for (M, K, N, xdt) in ((1, 3072, 12288, torch.float32), (16, 3072, 9216, torch.bfloat16)):
+        wbytes = K * N // 2 + (K // 128) * N * 4
+        copies = int(np.ceil(1.0e9 / wbytes))
+        ws = [B.from_packed(torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), dtype=torch.int32, device=dev,
+                                          generator=gen),
+                            torch.rand((K // 128, N), device=dev, generator=gen) * 0.015 + 0.005, 1, 128, (K, N))
+              for _ in range(copies)]
+        x = torch.randn((M, K), device=dev, generator=gen).to(xdt)
+        y = torch.empty((M, N), device=dev)
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            B.q_matmul(x, ws[0], out=y)  # sizes the stream's workspace outside capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for w in ws:
+                B.q_matmul(x, w, out=y)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / copies
+        nbytes = wbytes + M * K * x.element_size() + M * N * 4
+        out[f"{M}x{K}x{N}"] = {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+                               "frac_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
+                               "weight_copies": copies}
+        del ws, graph
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -191,6 +299,9 @@ def main():
     glu_ms = g0.elapsed_time(g1) / args.steps
     glu_fl = 2 * gemm_flops(M_TOKENS, Ku, Nu)
 
+    block_measured_ms = time_denoise_block(B, W, dev, weights, w3, args)
+    small_m = time_small_m(B, dev)
+
     gemm_ms = sum(per_op_ms[n] for n, _, _ in GEMMS)
     gemm_fl = sum(flops[n] for n, _, _ in GEMMS)
     attn_ms = per_op_ms["attention"]
@@ -203,8 +314,8 @@ def main():
     else:
         dom, dom_fl, dom_ms, dom_launches = "attention", flops["attention"], attn_ms, 1
     achieved = dom_fl / (dom_ms * 1e-3) / 1e12
-    # Denoise block (block.rs:84-134 via feed_forward.rs:32-36): QKV + attention + O + two SwiGLU
-    # up projections + down projection, from the measured kernel times (glue kernels excluded).
+    # Sum of the block's GEMM and attention kernels (block.rs:84-134 via feed_forward.rs:32-36):
+    # QKV + attention + O + two SwiGLU up projections + down, from the step's kernel times.
     block_ms = per_op_ms["qkv"] + attn_ms + per_op_ms["o"] + 2 * per_op_ms["mlp_up"] + per_op_ms["mlp_down"]
 
     result = {
@@ -226,10 +337,16 @@ def main():
                    "tokens": M_TOKENS, "hidden": 3072, "heads": 24, "head_dim": 128,
                    "parallelism": "single-gpu"},
         "frac_peak": round(step_flops / (ms_per_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-        "ms_per_denoise_block": round(block_ms, 4),
-        "ms_per_denoise_block_1xup": round(block_ms - per_op_ms["mlp_up"], 4),
-        "ms_per_denoise_block_fused_swiglu": round(
+        "ms_per_denoise_block": round(block_measured_ms, 4),
+        "denoise_block": ("SingleStreamBlock.forward measured end to end (events): modulation GEMV, "
+                          "3 glue passes, fused QKV, Q/K norm+RoPE, attention, O, fused SwiGLU, down; "
+                          "4608 tok x 3072, 24x128 heads, SwiGLU 12288, bf16 activations"),
+        "denoise_block_tflops": round(1.652e12 / (block_measured_ms * 1e-3) / 1e12, 2),
+        "ms_sum_block_kernels": round(block_ms, 4),
+        "ms_sum_block_kernels_1xup": round(block_ms - per_op_ms["mlp_up"], 4),
+        "ms_sum_block_kernels_fused_swiglu": round(
             per_op_ms["qkv"] + attn_ms + per_op_ms["o"] + glu_ms + per_op_ms["mlp_down"], 4),
+        "small_m": small_m,
         "per_kernel": per_kernel,
         "fused_swiglu": {"ms": round(glu_ms, 4), "tflops": round(glu_fl / (glu_ms * 1e-3) / 1e12, 2),
                          "frac_peak": round(glu_fl / (glu_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),

@@ -12,7 +12,8 @@ from .block import (DoubleStreamAttention, DoubleStreamBlock, GqaAttention, RmsN
 from .linear import (Linear, LuminaFeedForward, linear_forward, q_matmul, q_matmul_swiglu,
                      qwen_linear_forward)
 from .qwen import Qwen3VlTextAttention
-from .q4 import (BOOGU_DENOISER, FLUX_VAE, QWEN3_VL, Q4Weight, from_packed,
+from .q4 import (BOOGU_DENOISER, FLUX_VAE, QWEN3_VL, Q4Weight, from_packed, from_payload,
+                 payload_layout, split_payload,
                  q4s_storage_block_and_axis, q4s_stored_dtype, quantize_q4s_block128_f32,
                  quantize_row_layout_q4s_block_up_to128_f32)
 
@@ -24,7 +25,7 @@ __all__ = [
     "burn_attention", "check_cu_seqlens", "frame_ranges_to_cu_seqlens",
     "RmsNorm", "qk_norm_rope", "STRICT_F32", "F16_STORAGE_F32_ACCUM",
     "Linear", "LuminaFeedForward", "linear_forward", "q_matmul", "q_matmul_swiglu",
-    "qwen_linear_forward", "Q4Weight", "from_packed",
+    "qwen_linear_forward", "Q4Weight", "from_packed", "from_payload", "payload_layout", "split_payload",
     "q4s_storage_block_and_axis", "q4s_stored_dtype", "quantize_q4s_block128_f32",
     "quantize_row_layout_q4s_block_up_to128_f32", "BiqError", "InvalidArgument", "Unsupported",
     "block_glue", "RmsNormZero", "GqaAttention", "SingleStreamBlock", "DoubleStreamAttention",

@@ -41,12 +41,15 @@ SIGNATURES = {
     "biq_last_error": ([], ctypes.c_char_p),
     "biq_q4_storage_block": ([_I, _I64, _I64], _I),
     "biq_q4_stored_dtype": ([_I, _I64, _I64, ctypes.c_char_p, ctypes.c_size_t], _I),
+    "biq_q4_payload_layout": ([ctypes.c_char_p, _I64, _I64, _I64, ctypes.POINTER(_I), ctypes.POINTER(_I),
+                               ctypes.POINTER(_I64), ctypes.POINTER(_I64)], _I),
     "biq_q4_quantize": ([_P, _P, _I, _I64, _I64, _P, _P], _I),
     "biq_q4_dequant_f32": ([_P, _P, _P, _I, _I, _I64, _I64, _P], _I),
     "biq_q4_linear": ([_P, _P, _I, _I64, _I64, _I64, _P, _P, _I, _I, _I64, _P, _P, _I], _I),
     "biq_block_glue": ([_P, _I64, _I64, _I64, _P, _P, _I, _P, _P, _P, ctypes.c_float, _P, _P, _P,
                         ctypes.c_float, _P, _P, _I], _I),
     "biq_silu": ([_P, _I64, _P, _I, _P], _I),
+    "biq_release_stream_workspace": ([_P], _I),
     "biq_q4_linear_noalloc": ([_P, _P, _I, _I64, _I64, _I64, _P, _P, _I, _I, _I64, _P, _P, _I], _I),
     "biq_q4_linear_swiglu": ([_P, _P, _I, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _I], _I),
     "biq_attention": ([_P, _P, _P, _P, _P, _I, _I, _I64, _I64, _I64, _I64, _I64, _I64,

@@ -94,10 +94,11 @@ class RmsNormZero:
 @dataclass
 class GqaAttention:
     """attention.rs:700-833: bias-free to_q / to_k / to_v / to_out projections, per-head
-    strict-F32 RMSNorm + RoPE and grouped-query flash attention."""
-    to_q: Linear
-    to_k: Linear
-    to_v: Linear
+    strict-F32 RMSNorm + RoPE and grouped-query flash attention.  to_q / to_k / to_v may be None
+    when the packed `qkv` weight is given (self attention only)."""
+    to_q: Optional[Linear]
+    to_k: Optional[Linear]
+    to_v: Optional[Linear]
     to_out: Linear
     norm_q: RmsNorm
     norm_k: RmsNorm
@@ -105,16 +106,29 @@ class GqaAttention:
     kv_heads: int
     head_dim: int
     query_chunk_size: int = 8192
+    # Optional packed [K, (heads + 2 kv_heads) * head_dim] weight holding to_q | to_k | to_v
+    # column-wise: self attention then runs one projection GEMM and hands the prep kernel strided
+    # Q / K / V views of its output (the same products as the three projections).
+    qkv: Optional[Linear] = None
 
     def forward(self, query_tokens: torch.Tensor, key_value_tokens: torch.Tensor,
-                rope: Tuple[torch.Tensor, torch.Tensor]) -> torch.Tensor:
+                rope: Tuple[torch.Tensor, torch.Tensor],
+                out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """to_out(attention(norm+RoPE(q), norm+RoPE(k), v)); `out_dtype` is the dtype of the
+        attention output that feeds to_out (f32 by default, as the reference)."""
         B, Sq, _ = query_tokens.shape
         Sk = key_value_tokens.shape[1]
-        q = linear_forward(self.to_q, query_tokens).reshape(B, Sq, self.heads, self.head_dim)
-        k = linear_forward(self.to_k, key_value_tokens).reshape(B, Sk, self.kv_heads, self.head_dim)
-        v = linear_forward(self.to_v, key_value_tokens).reshape(B, Sk, self.kv_heads, self.head_dim)
+        H, Hkv, D = self.heads, self.kv_heads, self.head_dim
+        if self.qkv is not None and query_tokens is key_value_tokens:
+            fused = linear_forward(self.qkv, query_tokens).view(B, Sq, H + 2 * Hkv, D)
+            q, k, v = fused[:, :, :H], fused[:, :, H:H + Hkv], fused[:, :, H + Hkv:]
+        else:
+            q = linear_forward(self.to_q, query_tokens).reshape(B, Sq, H, D)
+            k = linear_forward(self.to_k, key_value_tokens).reshape(B, Sk, Hkv, D)
+            v = linear_forward(self.to_v, key_value_tokens).reshape(B, Sk, Hkv, D)
         out = NativeQ4FlashAttention.execute_gqa_with_qk_norm_rope(
-            q, k, v, self.norm_q, self.norm_k, rope, self.query_chunk_size)
+            q, k, v, self.norm_q, self.norm_k, rope, self.query_chunk_size,
+            out_dtype=out_dtype or torch.float32)
         return linear_forward(self.to_out, out.reshape(B, Sq, self.heads * self.head_dim))
 
 
@@ -125,7 +139,9 @@ class SingleStreamBlock:
         tokens = tokens + norm2(attn(normalized)) * tanh(gate_attn)
         tokens = tokens + ffn_norm2(ffn(ffn_norm1(tokens) * (1 + scale_mlp))) * tanh(gate_mlp)
     with the three glue steps fused into biq_block_glue passes.  `activation_dtype` is the dtype
-    the projections read (f32 as the reference; bf16 halves their input traffic)."""
+    the projections read -- the normalised tokens, the attention output and the FFN's gated
+    hidden state (f32 as the reference; bf16 halves their traffic and keeps the projections on
+    single-pass 16-bit matrix-core operands)."""
     norm1: RmsNormZero
     attn: GqaAttention
     norm2: RmsNorm
@@ -141,12 +157,12 @@ class SingleStreamBlock:
         scale_msa, gate_msa, scale_mlp, gate_mlp = self.norm1.modulation(conditioning, width)
         normalized = block_glue(tokens, next_norm=self.norm1.norm, next_scale=scale_msa,
                                 next_dtype=self.activation_dtype)
-        attended = self.attn.forward(normalized, normalized, rope).contiguous()
+        attended = self.attn.forward(normalized, normalized, rope, out_dtype=self.activation_dtype).contiguous()
         tokens1 = torch.empty_like(tokens)
         mlp_in = block_glue(attended, residual=tokens, branch_norm=self.norm2, gate=gate_msa,
                             residual_out=tokens1, next_norm=self.ffn_norm1, next_scale=scale_mlp,
                             next_dtype=self.activation_dtype)
-        mlp = self.feed_forward.forward(mlp_in).contiguous()
+        mlp = self.feed_forward.forward(mlp_in, hidden_dtype=self.activation_dtype).contiguous()
         out = torch.empty_like(tokens)
         block_glue(mlp, residual=tokens1, branch_norm=self.ffn_norm2, gate=gate_mlp, residual_out=out)
         return out

@@ -7,6 +7,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "common.h"
 
@@ -30,9 +31,11 @@ int check_launch(const char *what) {
 
 // One grow-only scratch buffer per (device, stream): calls on one stream run in order, so they
 // may share it; calls on different streams never do.  A buffer that is outgrown is kept, not
-// freed (a captured graph may still name it); all of them live until the process ends.
+// freed (a captured graph may still name it); all of them live until the process ends or
+// biq_release_stream_workspace releases the stream's buffers.
 static std::mutex g_ws_mutex;
 static std::map<std::pair<int, uintptr_t>, std::pair<void *, size_t>> g_ws;
+static std::map<std::pair<int, uintptr_t>, std::vector<void *>> g_ws_outgrown;
 
 int stream_workspace(hipStream_t s, size_t bytes, void **out) {
   int dev = 0;
@@ -51,6 +54,7 @@ int stream_workspace(hipStream_t s, size_t bytes, void **out) {
   want = (want + (1u << 20) - 1) & ~((size_t)(1u << 20) - 1);
   void *p = nullptr;
   if (hipMalloc(&p, want) != hipSuccess) return fail(BIQ_ERR_HIP, "workspace: hipMalloc failed");
+  if (e.first != nullptr) g_ws_outgrown[{dev, reinterpret_cast<uintptr_t>(s)}].push_back(e.first);
   e = {p, want};
   *out = p;
   return BIQ_OK;
@@ -80,9 +84,36 @@ int device_cu_count() {
   return n;
 }
 
+int release_stream_workspace(hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(BIQ_ERR_HIP, "workspace: no current device");
+  if (hipStreamSynchronize(s) != hipSuccess) return fail(BIQ_ERR_HIP, "workspace: stream synchronisation failed");
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  const std::pair<int, uintptr_t> key{dev, reinterpret_cast<uintptr_t>(s)};
+  int st = BIQ_OK;
+  auto it = g_ws.find(key);
+  if (it != g_ws.end()) {
+    if (hipFree(it->second.first) != hipSuccess) st = fail(BIQ_ERR_HIP, "workspace: hipFree failed");
+    g_ws.erase(it);
+  }
+  auto old = g_ws_outgrown.find(key);
+  if (old != g_ws_outgrown.end()) {
+    for (void *p : old->second)
+      if (hipFree(p) != hipSuccess) st = fail(BIQ_ERR_HIP, "workspace: hipFree failed");
+    g_ws_outgrown.erase(old);
+  }
+  return st;
+}
+
 }  // namespace biq
 
 extern "C" {
+
+// Frees the scratch kept for (current device, stream) after waiting for the stream.
+int biq_release_stream_workspace(void *stream) {
+  biq::clear_error();
+  return biq::release_stream_workspace(reinterpret_cast<hipStream_t>(stream));
+}
 
 const char *biq_version(void) { return "biq 0.1.0 gfx950"; }
 
@@ -115,6 +146,41 @@ int biq_q4_stored_dtype(int layout, int64_t rows, int64_t cols, char *buf, size_
   if (buf == nullptr || buf_len <= strlen(tmp))
     return biq::fail(BIQ_ERR_INVALID_ARG, "stored dtype buffer too small");
   memcpy(buf, tmp, strlen(tmp) + 1);
+  return BIQ_OK;
+}
+
+// Q4S tensor payload (the importer's single byte buffer: packed words, then f32 scales;
+// crates/burn_boogu/src/artifacts.rs:7276-7283,7364-7377) -> layout, block and byte split, after
+// checking the stored-dtype string and the size against the storage contract of the logical
+// shape (q4s_stored_dtype, artifacts.rs:513-536; boogu_import.rs:1693-1719).
+int biq_q4_payload_layout(const char *stored_dtype, int64_t rows, int64_t cols, int64_t payload_bytes,
+                          int *layout, int *block, int64_t *words_bytes, int64_t *scales_bytes) {
+  biq::clear_error();
+  if (!stored_dtype || !layout || !block || !words_bytes || !scales_bytes)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "null pointer argument");
+  int lay = -1;
+  if (strstr(stored_dtype, "-packed-axis0") != nullptr) lay = BIQ_Q4_NK_AXIS0;
+  else if (strstr(stored_dtype, "-packed-axis1") != nullptr) lay = BIQ_Q4_KN_AXIS1;
+  if (lay < 0 || strncmp(stored_dtype, "q4s-block", 9) != 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, std::string("not a Q4S stored dtype: ") + stored_dtype);
+  char expect[64];
+  if (biq_q4_stored_dtype(lay, rows, cols, expect, sizeof expect) != BIQ_OK)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "the logical shape has no Q4S storage contract for this layout");
+  if (strcmp(expect, stored_dtype) != 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, std::string("stored dtype ") + stored_dtype + " does not match " +
+                                              expect + " for this shape");
+  const int blk = biq_q4_storage_block(lay, rows, cols);
+  // logical [K, N] (axis 1) or [N, K] (axis 0); K is the packed and blocked axis
+  const int64_t K = lay == BIQ_Q4_KN_AXIS1 ? rows : cols;
+  const int64_t N = lay == BIQ_Q4_KN_AXIS1 ? cols : rows;
+  const int64_t wb = K * N / 2, sb = (K / blk) * N * 4;
+  if (payload_bytes != wb + sb)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "Q4S payload is " + std::to_string(payload_bytes) +
+                                              " bytes; the contract needs " + std::to_string(wb + sb));
+  *layout = lay;
+  *block = blk;
+  *words_bytes = wb;
+  *scales_bytes = sb;
   return BIQ_OK;
 }
 

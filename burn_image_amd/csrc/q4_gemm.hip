@@ -905,6 +905,9 @@ int check_linear(const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx, 
   // 256 packed columns of K / 8 words must span less than 2^31 bytes
   if (ldx >= (1LL << 21) || N >= (1LL << 24) || K >= (1LL << 24))
     return biq::fail(BIQ_ERR_UNSUPPORTED, "q4 linear: row stride, N or K too large for 32-bit tile offsets");
+  // the scale grid is addressed through one buffer descriptor with 32-bit offsets
+  if ((K / block) * N * 4 >= (1LL << 31))
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "q4 linear: the scale grid (K / block) * N * 4 bytes must stay below 2^31");
   const int esz = x_dtype == BIQ_DTYPE_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(x) & 15) || ((ldx * esz) & 15) ||
       (reinterpret_cast<uintptr_t>(words) & 15) || (reinterpret_cast<uintptr_t>(scales) & 3))

@@ -119,6 +119,43 @@ def from_packed(words: torch.Tensor, scales: torch.Tensor, layout: int, block: i
     return Q4Weight(words.contiguous(), scales.contiguous(), layout, block, (rows, cols))
 
 
+def payload_layout(stored_dtype: str, shape: Sequence[int], payload_bytes: int):
+    """(layout, block, words_bytes, scales_bytes) of a Q4S payload for a logical [rows, cols]
+    weight stored as `stored_dtype`, after libbiq checks the string and the size against the
+    storage contract (artifacts.rs:513-536,7276-7283,7364-7377; boogu_import.rs:1693-1719)."""
+    if len(shape) != 2:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "Q4S payloads hold rank-two matrices")
+    lay, blk = ctypes.c_int(), ctypes.c_int()
+    wb, sb = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(_lib.load().biq_q4_payload_layout(stored_dtype.encode(), int(shape[0]), int(shape[1]),
+                                                 int(payload_bytes), ctypes.byref(lay), ctypes.byref(blk),
+                                                 ctypes.byref(wb), ctypes.byref(sb)))
+    return lay.value, blk.value, wb.value, sb.value
+
+
+def split_payload(payload: torch.Tensor, stored_dtype: str, shape: Sequence[int]):
+    """Views (words int32, scales float32, layout, block) into a flat uint8 payload (host or
+    device) -- no copy: words [K/8, N] (axis 1) or [N, K/8] (axis 0), then scales."""
+    if payload.dtype != torch.uint8 or payload.dim() != 1 or not payload.is_contiguous():
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "a Q4S payload is a contiguous flat uint8 tensor")
+    lay, blk, wb, sb = payload_layout(stored_dtype, shape, payload.numel())
+    if payload.data_ptr() % 16 != 0:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "Q4S payloads must be 16-byte aligned")
+    rows, cols = int(shape[0]), int(shape[1])
+    K, N = (rows, cols) if lay == _lib.Q4_KN_AXIS1 else (cols, rows)
+    words = payload[:wb].view(torch.int32).view((K // 8, N) if lay == _lib.Q4_KN_AXIS1 else (N, K // 8))
+    scales = payload[wb:wb + sb].view(torch.float32).view((K // blk, N) if lay == _lib.Q4_KN_AXIS1 else (N, K // blk))
+    return words, scales, lay, blk
+
+
+def from_payload(payload: torch.Tensor, stored_dtype: str, shape: Tuple[int, int]) -> Q4Weight:
+    """A Q4Weight over a Q4S tensor payload resident on the GPU (the importer's values-then-scales
+    bytes, e.g. read from an artifact), without copying; the contract is checked first."""
+    _require_cuda(payload, "payload")
+    words, scales, lay, blk = split_payload(payload, stored_dtype, shape)
+    return Q4Weight(words, scales, lay, blk, (int(shape[0]), int(shape[1])))
+
+
 def quantize_row_layout_q4s_block_up_to128_f32(weight: torch.Tensor) -> Q4Weight:
     """GPU restatement of artifacts.rs:7296-7388 for a Boogu [input, output] matrix.
     F16 input is widened to F32 first, as the reference does."""

@@ -63,6 +63,19 @@ int biq_q4_storage_block(int layout, int64_t rows, int64_t cols);
  * Returns BIQ_ERR_INVALID_ARG if the shape has no Q4S contract or buf is too small. Host-only. */
 int biq_q4_stored_dtype(int layout, int64_t rows, int64_t cols, char *buf, size_t buf_len);
 
+/* Host-only: layout, block and byte split of a Q4S tensor payload -- the importer's single byte
+ * buffer of packed words followed by f32 scales (crates/burn_boogu/src/artifacts.rs:7276-7283,
+ * 7364-7377) -- for a logical [rows, cols] weight stored as `stored_dtype`
+ * ("q4s-block{b}-f32-packed-axis0" or "q4s-block{b}x1-f32-packed-axis1").  Checks the string
+ * and payload_bytes against the storage contract of the shape (biq_q4_stored_dtype; the
+ * importer's size contract, crates/burn_boogu/src/bin/boogu_import.rs:1693-1719) and returns
+ * BIQ_ERR_INVALID_ARG on any mismatch.  The words are the first words_bytes of the payload and
+ * the scales the next scales_bytes (4-byte aligned whenever the payload is): pass payload and
+ * payload + words_bytes to biq_q4_linear without copying. */
+int biq_q4_payload_layout(const char *stored_dtype, int64_t rows, int64_t cols,
+                          int64_t payload_bytes, int *layout, int *block, int64_t *words_bytes,
+                          int64_t *scales_bytes);
+
 /* Quantise an f32 weight on the GPU, byte-for-byte as the reference importer does.
  * layout BIQ_Q4_KN_AXIS1: w is [K, N] -> quantize_row_layout_q4s_block_up_to128_f32
  *   (artifacts.rs:7296-7388), block = biq_q4_storage_block(1, K, N).
@@ -96,6 +109,14 @@ int biq_q4_dequant_f32(void *stream, const uint32_t *words, const float *scales,
 int biq_q4_linear(void *stream, const void *x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   const uint32_t *words, const float *scales, int layout, int block, int64_t N,
                   const float *bias, void *y, int y_dtype);
+
+/* Releases the grow-only scratch the library keeps for (current device, stream) -- used by the
+ * small-M route and by K-split GEMM tails -- including buffers an earlier growth replaced.  It
+ * waits for the stream first.  Without this call the buffers live until the process ends (one
+ * set per stream that ever ran such a call); a runtime that creates and destroys streams should
+ * call it before destroying one.  The caller must ensure no captured graph still names the
+ * buffers (graphs record their addresses).  A later call on the stream allocates afresh. */
+int biq_release_stream_workspace(void *stream);
 
 /* Size of the static scratch biq_q4_linear_noalloc uses on each GPU (32 MiB). */
 #define BIQ_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)

@@ -28,11 +28,12 @@ def test_cpu_baseline_leg_fields(oracle):
         x_np[name] = W.activations(3, 2 * i, bench.M_TOKENS, K, "bf16")
     q_np, k_np, v_np = W.boogu_attention(2)
     rows = 32
-    r = bench.cpu_baseline(types.SimpleNamespace(cpu_rows=rows), words_np, scales_np, x_np,
+    r = bench.cpu_baseline(types.SimpleNamespace(cpu_rows=rows, cpu_runs=2), words_np, scales_np, x_np,
                            q_np, k_np, v_np)
     assert r["kind"] == "port" and r["unit"] == "TFLOP/s"
     assert r["cores"] >= 1 and r["value"] > 0
-    assert f"first {rows} of 4608 rows" in r["sample"]
+    assert f"first {rows} of 4608 rows" in r["sample"] and "median of 2 runs" in r["sample"]
+    assert "cpu_model" in r and r["nproc"] >= 1
     assert set(r["per_op_tflops"]) == {"qkv", "o", "mlp_up", "mlp_down", "attention"}
     step_flops = (sum(bench.gemm_flops(bench.M_TOKENS, K, N) for _, K, N in bench.GEMMS)
                   + bench.attn_flops(**bench.ATTN))

@@ -229,8 +229,8 @@ def test_gpu_q4_linear_small_m(gpu, oracle, layout, block, xdt, M):
 
 def test_gpu_q4_linear_small_m_bias_and_boundary(gpu, oracle):
     """Bias on the streaming route; M = 16 (streaming) and M = 17 (tiled MFMA route) agree with
-    the oracle on the same rows; a second call overwrites (the route accumulates atomically into
-    an output it first fills with the bias)."""
+    the oracle on the same rows; a second call overwrites the output (the route writes partial
+    rows per K chunk and an ordered reduction adds them and the bias into y)."""
     K, N = 3360, 840
     blk = oracle.q4_kn_block(K, N)
     x = W.activations(16, 1, 17, K, "bf16")
@@ -395,3 +395,49 @@ def test_gpu_q4_swiglu_released_width(gpu, oracle):
     ref = silu_gate_ref(oracle.q4_linear_f64(x, w1, s1, 1, blk, N, rows=rows),
                         oracle.q4_linear_f64(x, w3, s3, 1, blk, N, rows=rows))
     assert_parity(y[rows], ref, f"swiglu_released_{K}x{N}_blk{blk}")
+
+
+@pytest.mark.parametrize("layout", [1, 0])
+def test_gpu_q4_linear_on_loaded_payload(gpu, oracle, layout):
+    """An importer payload (words then scales, artifacts.rs:7364-7377) copied to the GPU as one
+    uint8 buffer runs the GEMM through zero-copy views, against the f64 oracle."""
+    rng = np.random.default_rng(95 + layout)
+    if layout == 1:
+        K, N = 3360, 840
+        w = (rng.standard_normal((K, N)) * 0.05).astype(np.float32)
+        words, scales, blk = oracle.q4_quantize_kn(w)
+        shape, dtype = (K, N), B.q4s_stored_dtype(B.BOOGU_DENOISER, (K, N))
+    else:
+        N, K = 1024, 4096
+        w = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+        words, scales = oracle.q4_quantize_nk(w)
+        blk = 128
+        shape, dtype = (N, K), B.q4s_stored_dtype(B.QWEN3_VL, (N, K))
+    payload = torch.from_numpy(np.frombuffer(words.astype("<u4").tobytes() + scales.astype("<f4").tobytes(),
+                                             np.uint8).copy()).to(gpu)
+    q = B.from_payload(payload, dtype, shape)
+    assert q.words.data_ptr() == payload.data_ptr() and q.block == blk and q.layout == layout
+    x = W.activations(15, layout, 200, K, "bf16")
+    y = B.q_matmul(dev(x, torch.bfloat16, gpu), q)
+    ref = oracle.q4_linear_f64(x, words, scales, layout, blk, N).astype(np.float32)
+    assert_parity(host(y), ref, f"payload_layout{layout}")
+
+
+def test_gpu_release_stream_workspace(gpu, oracle):
+    """biq_release_stream_workspace frees the scratch of a stream (after waiting for it); the next
+    call on that stream allocates again and gives the same bits."""
+    K, N, M = 3072, 1024, 5
+    x = W.activations(19, 1, M, K, "bf16")
+    words, scales = W.q4_weight(19, 2, K, N, layout=1)
+    q = weight(words, scales, 1, 128, K, N, gpu)
+    xd = dev(x, torch.bfloat16, gpu)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        y0 = B.q_matmul(xd, q)
+        B._lib.check(B._lib.load().biq_release_stream_workspace(stream.cuda_stream))
+        y1 = B.q_matmul(xd, q)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+    with torch.cuda.stream(stream):
+        B._lib.check(B._lib.load().biq_release_stream_workspace(stream.cuda_stream))
+    B._lib.check(B._lib.load().biq_release_stream_workspace(stream.cuda_stream))  # nothing left: fine
