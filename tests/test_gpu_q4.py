@@ -227,6 +227,25 @@ def test_gpu_q4_linear_small_m(gpu, oracle, layout, block, xdt, M):
     assert_parity(y, ref, f"smallm_M{M}_blk{block}_l{layout}_{xdt}")
 
 
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+@pytest.mark.parametrize("M, K, block", [(8, 1024, 128), (2, 256, 32), (5, 1048, 8), (8, 3360, 32)])
+def test_gpu_q4_linear_small_m_staged_edges(gpu, oracle, xdt, M, K, block):
+    """The [K/8, N] small-M kernel for M <= 8 stages the activations in LDS (f32 as hi parts in
+    MFMA rows 0..7 and lo parts in rows 8..15): M = 8 fills both halves; K = 256 gives fewer K
+    units than waves (idle waves still join the reduction); K = 3360 ends in a partial unit.  The
+    activations are a row-strided view (row stride > K) and N = 200 leaves a column tail."""
+    N = 200
+    x = W.activations(19, M + K, M, K, xdt)
+    words, scales = W.q4_weight(19, block + K, K, N, layout=1, block=block)
+    wide = torch.zeros((M, K + 40), dtype=TORCH_DT[xdt], device=gpu)
+    wide[:, 8:8 + K] = dev(x, TORCH_DT[xdt], gpu)
+    xv = wide[:, 8:8 + K]
+    assert xv.stride(0) == K + 40
+    y = host(B.q_matmul(xv, weight(words, scales, 1, block, K, N, gpu)))
+    ref = oracle.q4_linear_f64(x, words, scales, 1, block, N).astype(np.float32)
+    assert_parity(y, ref, f"smallm_staged_M{M}_K{K}_blk{block}_{xdt}")
+
+
 def test_gpu_q4_linear_small_m_bias_and_boundary(gpu, oracle):
     """Bias on the streaming route; M = 16 (streaming) and M = 17 (tiled MFMA route) agree with
     the oracle on the same rows; a second call overwrites the output (the route writes partial
