@@ -11,8 +11,9 @@
 //
 // rms(v) = sqrt(mean(v^2) + eps) over the row, reduced in f32 (rms_normalized, norm.rs:28-35;
 // Burn's nn::RmsNorm for the gamma product; RmsNormZero's modulation order, norm.rs:144-152).
-// b = row / rows_per_batch picks the batch element's gate / scale row.  One 256-thread
-// workgroup per row; the row is read from global memory once per pass (the re-reads hit L2).
+// b = row / rows_per_batch picks the batch element's gate / scale row.  One 256-thread workgroup
+// per row: rows of up to 4096 elements are held in registers (block_glue_row_kernel); wider rows
+// are read once per pass (block_glue_kernel; the re-reads mostly hit L2).
 #include <math.h>
 
 #include "common.h"
@@ -127,6 +128,113 @@ __global__ void __launch_bounds__(GT) block_glue_kernel(GlueArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// The same pass with the row held in registers (rows of up to 4096 elements, W % 4 == 0, 16-byte
+// aligned rows): one 256-thread workgroup per row, thread t holding the 4-vectors t, t + 256, ...
+// Every input of the row (branch, residual, modulation rows) is loaded up front with 16-byte
+// (f32) or 8-byte (16-bit) vector loads, so a row costs one memory round trip; the residual row r
+// stays in registers for the second norm.  Per element the arithmetic is the order of
+// block_glue_kernel; only the f32 summation order of the two row sums differs.
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int GR_MAXK = 4;  // vectors of 4 per thread: rows up to 256 * 4 * 4 = 4096 elements
+
+template <int DT>
+__device__ __forceinline__ f32x4_t load4(const void *p, int64_t v) {  // elements 4v .. 4v + 3
+  if constexpr (DT == BIQ_DTYPE_F32) {
+    return reinterpret_cast<const f32x4_t *>(p)[v];
+  } else {
+    const uint2 d = reinterpret_cast<const uint2 *>(p)[v];
+    if constexpr (DT == BIQ_DTYPE_BF16)
+      return f32x4_t{biq::bf16_lo_to_f32(d.x), biq::bf16_hi_to_f32(d.x), biq::bf16_lo_to_f32(d.y),
+                     biq::bf16_hi_to_f32(d.y)};
+    else
+      return f32x4_t{biq::f16_bits_to_f32((uint16_t)(d.x & 0xffffu)), biq::f16_bits_to_f32((uint16_t)(d.x >> 16)),
+                     biq::f16_bits_to_f32((uint16_t)(d.y & 0xffffu)), biq::f16_bits_to_f32((uint16_t)(d.y >> 16))};
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store4(void *p, int64_t v, const f32x4_t &x) {
+  if constexpr (DT == BIQ_DTYPE_F32) {
+    reinterpret_cast<f32x4_t *>(p)[v] = x;
+  } else if constexpr (DT == BIQ_DTYPE_BF16) {
+    uint2 d;
+    d.x = biq::f32_to_bf16_bits(x[0]) | (biq::f32_to_bf16_bits(x[1]) << 16);
+    d.y = biq::f32_to_bf16_bits(x[2]) | (biq::f32_to_bf16_bits(x[3]) << 16);
+    reinterpret_cast<uint2 *>(p)[v] = d;
+  } else {
+    uint2 d;
+    d.x = biq::pack_f16x2(x[0], x[1]);
+    d.y = biq::pack_f16x2(x[2], x[3]);
+    reinterpret_cast<uint2 *>(p)[v] = d;
+  }
+}
+
+template <int BDT, int NDT>  // branch dtype; next dtype (-1: no next output)
+__global__ void __launch_bounds__(GT) block_glue_row_kernel(GlueArgs a) {
+  __shared__ float red[GT / 64];
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / a.rows_per_batch;
+  const int64_t W = a.width, nv = W / 4;
+  const float inv_w = 1.0f / (float)W;
+  const int64_t rv = row * nv, bv = b * nv;  // vector offsets of the row and of its batch rows
+  auto row4 = [](const float *p, int64_t v) { return reinterpret_cast<const f32x4_t *>(p)[v]; };
+  const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+
+  f32x4_t u[GR_MAXK], xr[GR_MAXK];  // the modulated branch (then r) and the residual input
+#pragma unroll
+  for (int k = 0; k < GR_MAXK; ++k) {
+    const int64_t v = threadIdx.x + GT * k;
+    const bool in = v < nv;
+    u[k] = in ? load4<BDT>(a.branch, rv + v) : z;
+    xr[k] = (in && a.x) ? row4(a.x, rv + v) : z;
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < GR_MAXK; ++k) {
+    const int64_t v = threadIdx.x + GT * k;
+    if (v < nv) {
+      if (a.branch_scale) u[k] *= row4(a.branch_scale, bv + v) + 1.0f;
+      if (a.branch_shift) u[k] += row4(a.branch_shift, bv + v);
+      ss += u[k][0] * u[k][0] + u[k][1] * u[k][1] + u[k][2] * u[k][2] + u[k][3] * u[k][3];
+    }
+  }
+  float ss_r = ss;
+  if (a.x) {
+    const float rms_b = sqrtf(block_sum(ss, red) * inv_w + a.branch_eps);
+    ss_r = 0.0f;
+#pragma unroll
+    for (int k = 0; k < GR_MAXK; ++k) {
+      const int64_t v = threadIdx.x + GT * k;
+      if (v < nv) {
+        f32x4_t nb = u[k] / rms_b;
+        if (a.branch_gamma) nb *= row4(a.branch_gamma, v);
+        if (a.gate) {
+          const f32x4_t gt = row4(a.gate, bv + v);
+          nb *= f32x4_t{tanhf(gt[0]), tanhf(gt[1]), tanhf(gt[2]), tanhf(gt[3])};
+        }
+        const f32x4_t r = xr[k] + nb;
+        if (a.x_out) reinterpret_cast<f32x4_t *>(a.x_out)[rv + v] = r;
+        u[k] = r;
+        ss_r += r[0] * r[0] + r[1] * r[1] + r[2] * r[2] + r[3] * r[3];
+      }
+    }
+  }
+  if constexpr (NDT >= 0) {
+    const float rms_r = sqrtf(block_sum(ss_r, red) * inv_w + a.next_eps);
+#pragma unroll
+    for (int k = 0; k < GR_MAXK; ++k) {
+      const int64_t v = threadIdx.x + GT * k;
+      if (v < nv) {
+        f32x4_t n = u[k] / rms_r;
+        if (a.next_gamma) n *= row4(a.next_gamma, v);
+        if (a.next_scale) n *= row4(a.next_scale, bv + v) + 1.0f;
+        store4<NDT>(a.next_out, rv + v, n);
+      }
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t rows_per_batch,
@@ -149,8 +257,33 @@ extern "C" int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t
     return biq::fail(BIQ_ERR_INVALID_ARG, "block glue epsilons must be non-negative");
   GlueArgs a{rows, width, rows_per_batch, x, branch, branch_dtype, branch_scale, branch_shift, branch_gamma, branch_eps, gate,
              x_out, next_gamma, next_eps, next_scale, next_out, next_dtype};
-  hipLaunchKernelGGL(block_glue_kernel, dim3((unsigned)rows), dim3(GT), 0,
-                     reinterpret_cast<hipStream_t>(stream), a);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // wave-per-row form: rows of <= 4096 elements in whole 16-byte vectors, every row 16-byte aligned
+  auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  auto al8 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 7) == 0; };
+  const bool vec = width % 4 == 0 && width <= GT * 4 * GR_MAXK &&
+                   (branch_dtype == BIQ_DTYPE_F32 ? al16(branch) : al8(branch)) && al16(x) && al16(x_out) &&
+                   al16(branch_scale) && al16(branch_shift) && al16(branch_gamma) && al16(gate) &&
+                   al16(next_gamma) && al16(next_scale) &&
+                   (!next_out || (next_dtype == BIQ_DTYPE_F32 ? al16(next_out) : al8(next_out)));
+  if (vec) {
+    const dim3 grid((unsigned)rows);
+#define BIQ_GLUE(BD, ND) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND>), grid, dim3(GT), 0, s, a)
+#define BIQ_GLUE_N(BD)                                                                             \
+  do {                                                                                             \
+    if (!next_out) BIQ_GLUE(BD, -1);                                                               \
+    else if (next_dtype == BIQ_DTYPE_F32) BIQ_GLUE(BD, BIQ_DTYPE_F32);                             \
+    else if (next_dtype == BIQ_DTYPE_F16) BIQ_GLUE(BD, BIQ_DTYPE_F16);                             \
+    else BIQ_GLUE(BD, BIQ_DTYPE_BF16);                                                             \
+  } while (0)
+    if (branch_dtype == BIQ_DTYPE_F32) BIQ_GLUE_N(BIQ_DTYPE_F32);
+    else if (branch_dtype == BIQ_DTYPE_F16) BIQ_GLUE_N(BIQ_DTYPE_F16);
+    else BIQ_GLUE_N(BIQ_DTYPE_BF16);
+#undef BIQ_GLUE_N
+#undef BIQ_GLUE
+    return biq::check_launch("block glue");
+  }
+  hipLaunchKernelGGL(block_glue_kernel, dim3((unsigned)rows), dim3(GT), 0, s, a);
   return biq::check_launch("block glue");
 }
 

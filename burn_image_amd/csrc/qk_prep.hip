@@ -8,7 +8,8 @@
 // The rotate-half layout restates Qwen's q_norm / k_norm (Burn nn::RmsNorm) followed by
 // apply_text_rope (crates/burn_qwen3_vl/src/text.rs:112-125,407-440).
 //
-// Per row (one wave; lane p owns the elements d = 2p, 2p + 1), F = the input type, rnd = rounding
+// Per row (one wave holds PREP_ROWS consecutive rows; lane p owns the elements d = 2p, 2p + 1 of
+// each), F = the input type, rnd = rounding
 // to F (identity for F32 inputs):
 //   rms   = sqrt(sum_d x_d^2 / D + eps)                  f32 (x widened to f32)
 //   n_d   = rnd(rnd(x_d / rnd(rms)) * rnd(gamma_d))      in F: the f32 rms is cast to F first
@@ -79,59 +80,99 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Position of a row of the fused index space (Q rows, then K rows, then V rows; each [B, S, H]
+// with the head fastest), stepped along a wave's rows without a division.
+struct RowLoc {
+  int kind;  // 0 = Q, 1 = K, 2 = V, 3 = past the end
+  int64_t r, h, s, b, H;
+};
+
+__device__ __forceinline__ RowLoc locate(const PrepArgs &p, int64_t row) {
+  const int64_t q_rows = p.B * p.S * p.Hq, kv_rows = p.B * p.S * p.Hkv;
+  RowLoc L;
+  if (row < q_rows) { L.kind = 0; L.r = row; L.H = p.Hq; }
+  else if (row < q_rows + kv_rows) { L.kind = 1; L.r = row - q_rows; L.H = p.Hkv; }
+  else if (row < q_rows + 2 * kv_rows) { L.kind = 2; L.r = row - q_rows - kv_rows; L.H = p.Hkv; }
+  else { L.kind = 3; L.r = 0; L.H = 1; }
+  L.h = L.r % L.H;
+  L.s = (L.r / L.H) % p.S;
+  L.b = L.r / (L.H * p.S);
+  return L;
+}
+
+__device__ __forceinline__ void advance(const PrepArgs &p, RowLoc &L) {
+  if (L.kind == 3) return;
+  ++L.r;
+  if (++L.h < L.H) return;
+  L.h = 0;
+  if (++L.s < p.S) return;
+  L.s = 0;
+  if (++L.b < p.B) return;
+  L = RowLoc{L.kind + 1, 0, 0, 0, 0, p.Hkv};  // next kind (K and V both have Hkv heads)
+}
+
+constexpr int PREP_ROWS = 8;  // rows per wave: their loads are all in flight before the first use
+
 template <typename InT, bool HALF>
 __global__ void __launch_bounds__(256) qk_prep_kernel(PrepArgs p, int out_bf16) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t q_rows = p.B * p.S * p.Hq, kv_rows = p.B * p.S * p.Hkv;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t pairs = p.D / 2;
   const bool active = lane < pairs;
   const int d = 2 * lane;
 
-  int kind;      // 0 = Q, 1 = K, 2 = V
-  int64_t r, H;
-  if (row < q_rows) { kind = 0; r = row; H = p.Hq; }
-  else if (row < q_rows + kv_rows) { kind = 1; r = row - q_rows; H = p.Hkv; }
-  else if (row < q_rows + 2 * kv_rows) { kind = 2; r = row - q_rows - kv_rows; H = p.Hkv; }
-  else return;
-  const int64_t h = r % H, s = (r / H) % p.S, b = r / (H * p.S);
-  const int64_t *st = kind == 0 ? p.qs : (kind == 1 ? p.ks : p.vs);
-  const InT *src = reinterpret_cast<const InT *>(kind == 0 ? p.q : (kind == 1 ? p.k : p.v)) +
-                   b * st[0] + s * st[1] + h * st[2];
-  uint16_t *dst = reinterpret_cast<uint16_t *>(kind == 0 ? p.qo : (kind == 1 ? p.ko : p.vo)) +
-                  r * p.D;
+  RowLoc L0 = locate(p, wave * PREP_ROWS);
+  RowLoc L = L0;
+  float2 x[PREP_ROWS];
+#pragma unroll
+  for (int i = 0; i < PREP_ROWS; ++i) {
+    x[i] = make_float2(0.0f, 0.0f);
+    if (L.kind < 3) {
+      const int64_t *st = L.kind == 0 ? p.qs : (L.kind == 1 ? p.ks : p.vs);
+      const InT *src = reinterpret_cast<const InT *>(L.kind == 0 ? p.q : (L.kind == 1 ? p.k : p.v)) +
+                       L.b * st[0] + L.s * st[1] + L.h * st[2];
+      if (active) x[i] = load_pair<InT>(src + d);
+    }
+    advance(p, L);
+  }
 
-  float2 x = active ? load_pair<InT>(src + d) : make_float2(0.0f, 0.0f);
-  if (kind == 2) {
-    if (active) *reinterpret_cast<uint32_t *>(dst + d) = store_bits(x.x, x.y, out_bf16);
-    return;
+  L = L0;
+#pragma unroll
+  for (int i = 0; i < PREP_ROWS; ++i, advance(p, L)) {
+    if (L.kind == 3) break;
+    uint16_t *dst = reinterpret_cast<uint16_t *>(L.kind == 0 ? p.qo : (L.kind == 1 ? p.ko : p.vo)) +
+                    L.r * p.D;
+    if (L.kind == 2) {
+      if (active) *reinterpret_cast<uint32_t *>(dst + d) = store_bits(x[i].x, x[i].y, out_bf16);
+      continue;
+    }
+    const float sum_sq = wave_sum(x[i].x * x[i].x + x[i].y * x[i].y);  // wave-uniform
+    const float eps = L.kind == 0 ? p.q_eps : p.k_eps;
+    const float rms = rnd<InT>(sqrtf(sum_sq / (float)p.D + eps));
+    const float *g = L.kind == 0 ? p.q_gamma : p.k_gamma;
+    const float n0 = active ? rnd<InT>(rnd<InT>(x[i].x / rms) * rnd<InT>(g[d])) : 0.0f;
+    const float n1 = active ? rnd<InT>(rnd<InT>(x[i].y / rms) * rnd<InT>(g[d + 1])) : 0.0f;
+    const float *cs = p.cos + L.b * p.rope_bs + L.s * p.D;
+    const float *sn = p.sin + L.b * p.rope_bs + L.s * p.D;
+    float y0 = 0.0f, y1 = 0.0f;
+    if constexpr (HALF) {
+      // partner elements d + h (first half) or d - h (second half) sit in lane p +- h / 2; every
+      // lane takes part in the shuffles (D % 4 == 0, host check)
+      const int hp = (int)(p.D / 4);
+      const int src = d < 2 * hp ? lane + hp : lane - hp;
+      const float m0 = __shfl(n0, src), m1 = __shfl(n1, src);
+      if (active) {
+        const float r0 = d < 2 * hp ? -m0 : m0, r1 = d < 2 * hp ? -m1 : m1;
+        y0 = rnd<InT>(n0 * cs[d] + r0 * sn[d]);
+        y1 = rnd<InT>(n1 * cs[d + 1] + r1 * sn[d + 1]);
+      }
+    } else if (active) {
+      y0 = rnd<InT>(rnd<InT>(n0 * rnd<InT>(cs[d])) + rnd<InT>(-n1 * rnd<InT>(sn[d])));
+      y1 = rnd<InT>(rnd<InT>(n1 * rnd<InT>(cs[d + 1])) + rnd<InT>(n0 * rnd<InT>(sn[d + 1])));
+    }
+    if (active) *reinterpret_cast<uint32_t *>(dst + d) = store_bits(y0, y1, out_bf16);
   }
-  const float sum_sq = wave_sum(x.x * x.x + x.y * x.y);  // wave-uniform
-  const float eps = kind == 0 ? p.q_eps : p.k_eps;
-  const float rms = rnd<InT>(sqrtf(sum_sq / (float)p.D + eps));
-  const float *g = kind == 0 ? p.q_gamma : p.k_gamma;
-  const float n0 = active ? rnd<InT>(rnd<InT>(x.x / rms) * rnd<InT>(g[d])) : 0.0f;
-  const float n1 = active ? rnd<InT>(rnd<InT>(x.y / rms) * rnd<InT>(g[d + 1])) : 0.0f;
-  const float *cs = p.cos + b * p.rope_bs + s * p.D;
-  const float *sn = p.sin + b * p.rope_bs + s * p.D;
-  float y0, y1;
-  if constexpr (HALF) {
-    // partner elements d + h (first half) or d - h (second half) sit in lane p +- h / 2; every
-    // lane takes part in the shuffles (D % 4 == 0, host check)
-    const int hp = (int)(p.D / 4);
-    const int src = d < 2 * hp ? lane + hp : lane - hp;
-    const float m0 = __shfl(n0, src), m1 = __shfl(n1, src);
-    if (!active) return;
-    const float r0 = d < 2 * hp ? -m0 : m0, r1 = d < 2 * hp ? -m1 : m1;
-    y0 = rnd<InT>(n0 * cs[d] + r0 * sn[d]);
-    y1 = rnd<InT>(n1 * cs[d + 1] + r1 * sn[d + 1]);
-  } else {
-    if (!active) return;
-    y0 = rnd<InT>(rnd<InT>(n0 * rnd<InT>(cs[d])) + rnd<InT>(-n1 * rnd<InT>(sn[d])));
-    y1 = rnd<InT>(rnd<InT>(n1 * rnd<InT>(cs[d + 1])) + rnd<InT>(n0 * rnd<InT>(sn[d + 1])));
-  }
-  *reinterpret_cast<uint32_t *>(dst + d) = store_bits(y0, y1, out_bf16);
 }
 
 }  // namespace
@@ -184,7 +225,7 @@ extern "C" int biq_qk_norm_rope(void *stream, const void *q, const void *k, cons
   a.B = B; a.S = S; a.Hq = Hq; a.Hkv = Hkv; a.D = D;
   a.qo = q_out; a.ko = k_out; a.vo = v_out;
   const int64_t rows = B * S * (Hq + 2 * Hkv);
-  const int64_t blocks = (rows + 3) / 4;
+  const int64_t blocks = (rows + 4 * PREP_ROWS - 1) / (4 * PREP_ROWS);
   if (blocks > 0x7fffffff) return biq::fail(BIQ_ERR_UNSUPPORTED, "fused preparation grid too large");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int ob = out_dtype == BIQ_DTYPE_BF16;

@@ -5,6 +5,8 @@
     python -m burn_image_amd.perf attention --B 1 --H 24 --Hkv 24 --S 4608 --D 128 [--dtype bf16]
                                             [--causal] [--segments 1024:64:512]
     python -m burn_image_amd.perf qk_prep --S 4608 --Hq 24 --Hkv 24 --D 128 [--dtype f32]
+    python -m burn_image_amd.perf glue --S 4608 --W 3072 [--dtype bf16]
+    python -m burn_image_amd.perf block --S 4608   (SingleStreamBlock.forward, 3072 wide)
     python -m burn_image_amd.perf copy --mib 512   (a plain device copy of known size: the
                                                     calibration kernel for HBM byte counters)
     (every op also takes --iters, --warmup and --graph)
@@ -151,6 +153,61 @@ def bench_qk_prep(a) -> dict:
             "frac_hbm_peak": round(bytes_ / us / 1e3 / PEAK_GBS, 4)}
 
 
+def bench_glue(a) -> dict:
+    """The block's middle glue pass (block.rs:91-111): r = x + rmsnorm(branch) * tanh(gate) into a
+    new residual, then rmsnorm(r) * (1 + scale) in bf16 for the next projection."""
+    from .block import block_glue
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    S, Wd = a.S, a.W
+    branch = torch.randn((1, S, Wd), device=dev, generator=g).to(DT[a.dtype])
+    x = torch.randn((1, S, Wd), device=dev, generator=g)
+    r = torch.empty_like(x)
+    gate = torch.randn((1, Wd), device=dev, generator=g)
+    scale = torch.randn((1, Wd), device=dev, generator=g)
+    n1, n2 = RmsNorm(torch.ones(Wd, device=dev)), RmsNorm(torch.ones(Wd, device=dev))
+    us = _time(lambda i: block_glue(branch, residual=x, branch_norm=n1, gate=gate, residual_out=r,
+                                    next_norm=n2, next_scale=scale, next_dtype=torch.bfloat16),
+               a.iters, a.warmup)
+    esz = {"f32": 4, "f16": 2, "bf16": 2}[a.dtype]
+    bytes_ = S * Wd * (esz + 4 + 4 + 2)  # branch and residual in, residual and bf16 rows out
+    return {"op": "glue", "S": S, "W": Wd, "dtype": a.dtype, "us": round(us, 3),
+            "gbs": round(bytes_ / us / 1e3, 1), "frac_hbm_peak": round(bytes_ / us / 1e3 / PEAK_GBS, 4)}
+
+
+def bench_block(a) -> dict:
+    """SingleStreamBlock.forward (block.rs:84-134) at S tokens x 3072, 24 x 128 heads, SwiGLU
+    12288, bf16 activations, random packed weights: modulation GEMV, three glue passes, fused
+    QKV, Q/K norm + RoPE, attention, O, fused SwiGLU, down (eager launches, as a caller runs it)."""
+    from . import block as BL
+    from . import linear as LN
+    from . import rope as R
+    from .workloads import boogu_joint_ids
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    Wd, H, D, C, F = 3072, 24, 128, 1024, 12288
+
+    def q4(K, N):
+        words = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), dtype=torch.int32, device=dev, generator=g)
+        scales = torch.rand((K // 128, N), device=dev, generator=g) * 0.015 + 0.005
+        return from_packed(words, scales, 1, 128, (K, N))
+    ones = lambda n: torch.ones(n, device=dev)  # noqa: E731
+    attn = BL.GqaAttention(None, None, None, LN.Linear(q4(Wd, Wd)), RmsNorm(ones(D)), RmsNorm(ones(D)),
+                           H, H, D, qkv=LN.Linear(q4(Wd, 3 * Wd)))
+    blk = BL.SingleStreamBlock(
+        norm1=BL.RmsNormZero(LN.Linear(q4(C, 4 * Wd), torch.zeros(4 * Wd, device=dev)), RmsNorm(ones(Wd))),
+        attn=attn, norm2=RmsNorm(ones(Wd)), ffn_norm1=RmsNorm(ones(Wd)), ffn_norm2=RmsNorm(ones(Wd)),
+        feed_forward=BL.LuminaFeedForward(LN.Linear(q4(Wd, F)), LN.Linear(q4(F, Wd)), LN.Linear(q4(Wd, F))),
+        activation_dtype=torch.bfloat16)
+    ids = boogu_joint_ids(2)[: a.S]
+    cos, sin = R.rope_values(ids, [32, 48, 48], 1.0e4)
+    rope = (torch.from_numpy(cos[None]).to(dev), torch.from_numpy(sin[None]).to(dev))
+    tokens = torch.randn((1, a.S, Wd), device=dev, generator=g)
+    cond = torch.randn((1, C), device=dev, generator=g)
+    us = _time(lambda i: blk.forward(tokens, rope, cond), a.iters, a.warmup)
+    return {"op": "block", "S": a.S, "hidden": Wd, "heads": H, "head_dim": D, "ffn": F, "us": round(us, 3)}
+
+
 def bench_copy(a) -> dict:
     dev = torch.device("cuda:0")
     n = a.mib << 20
@@ -190,6 +247,12 @@ def main(argv=None):
     p.add_argument("--Hkv", type=int, default=24)
     p.add_argument("--D", type=int, default=128)
     p.add_argument("--dtype", default="f32", choices=list(DT))
+    p = sub.add_parser("glue")
+    p.add_argument("--S", type=int, default=4608)
+    p.add_argument("--W", type=int, default=3072)
+    p.add_argument("--dtype", default="bf16", choices=list(DT))
+    p = sub.add_parser("block")
+    p.add_argument("--S", type=int, default=4608)
     p = sub.add_parser("copy")
     p.add_argument("--mib", type=int, default=512)
     for p in sub.choices.values():
@@ -201,7 +264,7 @@ def main(argv=None):
     _GRAPH = a.graph
     _lib.load()
     fn = {"q4_linear": bench_q4_linear, "attention": bench_attention, "qk_prep": bench_qk_prep,
-          "copy": bench_copy}[a.op]
+          "glue": bench_glue, "block": bench_block, "copy": bench_copy}[a.op]
     print(json.dumps(fn(a)), flush=True)
 
 
