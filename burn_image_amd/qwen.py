@@ -50,7 +50,7 @@ class Qwen3VlTextAttention:
         """hidden_states [B, S, hidden]; cos / sin [1 or B, S, head_dim] (rotate-half tables);
         attention_mask [B, S] bool (True = valid token) or None.  Rows of a left-padded prompt
         that see no valid key take the mean of V over every key, as the reference's
-        mask_fill(-1e30) softmax gives them (text.rs:176-178).  Returns [B, S, hidden] f32."""
+        mask_fill(-1e30) softmax gives them (text.rs:177-182).  Returns [B, S, hidden] f32."""
         Bn, S, _ = hidden_states.shape
         H, Hkv, D = self.num_heads, self.num_key_value_heads, self.head_dim
         if H % Hkv != 0:

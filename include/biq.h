@@ -174,7 +174,7 @@ int biq_silu(void *stream, int64_t n, const void *x, int x_dtype, float *y);
  *   crates/burn_qwen3_vl/src/text.rs:163-170); a query row left with no visible key is zero.
  * BIQ_KEY_MASK_VALID_FILL_MEAN: as VALID, but a row with no visible key gets the mean of V over
  *   all Skv keys -- what the reference's `mask_fill(-1e30)` then softmax gives for such a row
- *   (text.rs:176-178: every score equal, uniform weights), e.g. the left-padding rows of a batch.
+ *   (text.rs:177-182: every score equal, uniform weights), e.g. the left-padding rows of a batch.
  * BIQ_KEY_MASK_MASKED: a nonzero byte masks its key out (Burn's bool attention mask polarity);
  *   a row with no visible key is zero. */
 #define BIQ_KEY_MASK_VALID 0

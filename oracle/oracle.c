@@ -268,7 +268,7 @@ static inline int visible(int64_t i, int64_t j, int causal, const int32_t *cu, i
  * `attention_mask`, OR-ed into the causal mask as `valid.bool_not()` broadcast over queries
  * (crates/burn_qwen3_vl/src/text.rs:163-176).  A row left with no visible key gets, with
  * fill_mean, the mean of V over all Skv keys (softmax of a row filled with -1e30 everywhere is
- * uniform, text.rs:176-178), and zeros without it.
+ * uniform, text.rs:177-182), and zeros without it.
  * rows: query indices evaluated (NULL = all Sq). */
 void orc_attention_f64(const float *q, const float *k, const float *v, int64_t B, int64_t Hq,
                        int64_t Hkv, int64_t Sq, int64_t Skv, int64_t D, int64_t Dv, double scale,

@@ -178,7 +178,7 @@ def attention_f64(q, k, v, scale=None, causal=False, cu_seqlens=None, rows=None,
                   fill_mean=False):
     """Exact float64 attention over [B, H, S, D] inputs (GQA when k/v have fewer heads).
     key_valid: optional [B, Skv] bool (True = the key may be attended, Qwen's attention_mask);
-    rows left without a visible key get mean(V) with `fill_mean` (text.rs:176-178), else 0."""
+    rows left without a visible key get mean(V) with `fill_mean` (text.rs:177-182), else 0."""
     q = _c(q, np.float32)
     k = _c(k, np.float32)
     v = _c(v, np.float32)

@@ -116,7 +116,7 @@ def test_attention_key_mask_mode_validation():
 ])
 def test_cu_seqlens_host_validator(cu, S, ok):
     """Host-side segment table check (a malformed table never reaches the kernel through the
-    Python API; vision.rs:319-325 holds its frame ranges on the host)."""
+    Python API; the reference holds its frame ranges on the host, vision.rs:53-78,344-345)."""
     import burn_image_amd as B
     if ok:
         B.check_cu_seqlens(cu, S)

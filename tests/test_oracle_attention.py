@@ -187,7 +187,7 @@ def test_key_mask_equals_attention_over_kept_keys_correctness(oracle):
 def test_key_mask_left_padding_causal_rows_correctness(oracle):
     """Left padding (processor.rs:379-385) under the causal mask: row i >= pad equals causal
     attention over keys [pad, i]; rows i < pad see no key and average V over every key with the
-    reference's -1e30 fill (text.rs:176-178), or are zero without it."""
+    reference's -1e30 fill (text.rs:177-182), or are zero without it."""
     rng = np.random.default_rng(12)
     S, pad = 10, 3
     q = rng.standard_normal((1, 2, S, 8)).astype(np.float32)
