@@ -178,18 +178,20 @@ def time_denoise_block(B, W, dev, weights, w3, args):
 
 
 def time_small_m(B, dev):
-    """The small-M route at the modulation row (1 x 3072 x 12288, f32 activations) and at
-    16 x 3072 x 9216 (bf16 activations), each over >= 1 GB of distinct weights (the 256 MB MALL
-    cannot hold them), replayed from a HIP graph; GB/s = algorithmic bytes / time."""
+    """The small-M route at the modulation rows (1 x 3072 x 12288 block 128, the 3072-wide step's
+    RmsNormZero projection, and 1 x 3360 x 13440 block 32, the released model's; f32 activations)
+    and at 16 x 3072 x 9216 (bf16 activations), each over >= 1 GB of distinct weights (the 256 MB
+    MALL cannot hold them), replayed from a HIP graph; GB/s = algorithmic bytes / time."""
     import torch
     out = {}
     gen = torch.Generator(device=dev).manual_seed(11)
-    for (M, K, N, xdt) in ((1, 3072, 12288, torch.float32), (16, 3072, 9216, torch.bfloat16)):
-        wbytes = K * N // 2 + (K // 128) * N * 4
+    for (M, K, N, blk, xdt) in ((1, 3072, 12288, 128, torch.float32), (1, 3360, 13440, 32, torch.float32),
+                                (16, 3072, 9216, 128, torch.bfloat16)):
+        wbytes = K * N // 2 + (K // blk) * N * 4
         copies = int(np.ceil(1.0e9 / wbytes))
         ws = [B.from_packed(torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), dtype=torch.int32, device=dev,
                                           generator=gen),
-                            torch.rand((K // 128, N), device=dev, generator=gen) * 0.015 + 0.005, 1, 128, (K, N))
+                            torch.rand((K // blk, N), device=dev, generator=gen) * 0.015 + 0.005, 1, blk, (K, N))
               for _ in range(copies)]
         x = torch.randn((M, K), device=dev, generator=gen).to(xdt)
         y = torch.empty((M, N), device=dev)
@@ -210,7 +212,7 @@ def time_small_m(B, dev):
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / copies
         nbytes = wbytes + M * K * x.element_size() + M * N * 4
-        out[f"{M}x{K}x{N}"] = {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+        out[f"{M}x{K}x{N}" + ("" if blk == 128 else f"_blk{blk}")] = {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
                                "frac_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
                                "weight_copies": copies}
         del ws, graph

@@ -332,21 +332,21 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
     // first MFMA.)
     load_tile(kv0 + NS * BKV, RS[tt]);
 
-    // ---- S^T = K Q^T for the tile's 64 keys (2 x 32)
-    floatx16_t sacc[2];
+    // ---- S^T = K Q^T for the tile's 64 keys (2 x 32).  The two 32-key halves are independent
+    //      accumulator chains; d-steps outermost alternates them, so consecutive MFMAs never
+    //      wait for each other's result.
+    floatx16_t sacc[2] = {biq::zero16(), biq::zero16()};
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      floatx16_t a = biq::zero16();
+    for (int s = 0; s < DP / 16; ++s) {
 #pragma unroll
-      for (int s = 0; s < DP / 16; ++s) {
+      for (int ks = 0; ks < 2; ++ks) {
         const u32x4_t kf = *reinterpret_cast<const u32x4_t *>(
             &Ks[buf][(32 * ks + l32) * KS_LD + 16 * s + 8 * lh]);
         if constexpr (BF16)
-          a = biq::mfma32x32x16_bf16(biq::bitcast<bf16x8_t>(kf), biq::bitcast<bf16x8_t>(qf[s]), a);
+          sacc[ks] = biq::mfma32x32x16_bf16(biq::bitcast<bf16x8_t>(kf), biq::bitcast<bf16x8_t>(qf[s]), sacc[ks]);
         else
-          a = biq::mfma32x32x16_f16(biq::bitcast<half8_t>(kf), biq::bitcast<half8_t>(qf[s]), a);
+          sacc[ks] = biq::mfma32x32x16_f16(biq::bitcast<half8_t>(kf), biq::bitcast<half8_t>(qf[s]), sacc[ks]);
       }
-      sacc[ks] = a;
     }
 
     // ---- mask where the tile needs it; row max of the raw scores (the positive scale commutes
