@@ -177,6 +177,63 @@ def time_denoise_block(B, W, dev, weights, w3, args):
     return float(np.mean([e0.elapsed_time(e1) for e0, e1 in evs]))
 
 
+def time_released(B, dev):
+    """The reference's own throughput harnesses, at the released model's geometry:
+    * packed-Q4 projection 9261 x 3360 x 3360, f32 activations, weights quantised from the
+      harness's pattern by the Boogu quantizer (block 32 for K = 3360), fastest of 3 timed calls
+      after a warm-up (artifacts.rs:10588-10655);
+    * the 1.5K fused Q/K norm + RoPE + attention, 28 query / 4 key-value heads, S = 18579, D = 120,
+      f32 in and out, median of 5 timed calls after a warm-up (native_flash.rs:3736-3823; here
+      through execute_gqa_with_qk_norm_rope on token-major tensors).
+    Events around each call on the current stream."""
+    import torch
+    out = {}
+    stream = torch.cuda.current_stream(dev)
+    gen = torch.Generator(device=dev).manual_seed(13)
+
+    def timed(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(n):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms.append(e0.elapsed_time(e1))
+        return ms
+
+    M, K, N = 9261, 3360, 3360
+    idx = torch.arange(K * N, device=dev)
+    w = ((((idx // N) + (idx % N) * 3) % 15).to(torch.float32) - 7.0) * (1.0 / 64.0)
+    q = B.quantize_row_layout_q4s_block_up_to128_f32(w.reshape(K, N))
+    x = torch.randn((M, K), device=dev, generator=gen)
+    y = torch.empty((M, N), device=dev)
+    ms = min(timed(lambda: B.q_matmul(x, q, out=y), 3))
+    fl = gemm_flops(M, K, N)
+    out["q4_9261x3360x3360"] = {"ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+                                "frac_peak": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                                "block": q.block, "x_dtype": "f32", "timing": "fastest of 3"}
+    del x, y, q, w, idx
+    S, Hq, Hkv, D = 18579, 28, 4, 120
+    qt = torch.randn((1, S, Hq, D), device=dev, generator=gen)
+    kt = torch.randn((1, S, Hkv, D), device=dev, generator=gen)
+    vt = torch.randn((1, S, Hkv, D), device=dev, generator=gen)
+    nq, nk = B.RmsNorm(torch.ones(D, device=dev)), B.RmsNorm(torch.ones(D, device=dev))
+    rope = (torch.ones((1, S, D), device=dev), torch.zeros((1, S, D), device=dev))
+    run = lambda: B.NativeQ4FlashAttention.execute_gqa_with_qk_norm_rope(qt, kt, vt, nq, nk, rope, 16384)  # noqa: E731
+    ms = float(np.median(timed(run, 5)))
+    fl = attn_flops(B=1, H=Hq, S=S, D=D)
+    out["attention_1k5_s18579_h28_kv4_d120"] = {
+        "ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+        "frac_peak": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "includes": "fused Q/K norm + RoPE prep (f32 -> f16) and attention (f32 out)", "timing": "median of 5"}
+    del qt, kt, vt
+    torch.cuda.empty_cache()
+    return out
+
+
 def time_small_m(B, dev):
     """The small-M route at the modulation rows (1 x 3072 x 12288 block 128, the 3072-wide step's
     RmsNormZero projection, and 1 x 3360 x 13440 block 32, the released model's; f32 activations)
@@ -303,6 +360,7 @@ def main():
 
     block_measured_ms = time_denoise_block(B, W, dev, weights, w3, args)
     small_m = time_small_m(B, dev)
+    released = time_released(B, dev)
 
     gemm_ms = sum(per_op_ms[n] for n, _, _ in GEMMS)
     gemm_fl = sum(flops[n] for n, _, _ in GEMMS)
@@ -349,6 +407,7 @@ def main():
         "ms_sum_block_kernels_fused_swiglu": round(
             per_op_ms["qkv"] + attn_ms + per_op_ms["o"] + glu_ms + per_op_ms["mlp_down"], 4),
         "small_m": small_m,
+        "released_geometry": released,
         "per_kernel": per_kernel,
         "fused_swiglu": {"ms": round(glu_ms, 4), "tflops": round(glu_fl / (glu_ms * 1e-3) / 1e12, 2),
                          "frac_peak": round(glu_fl / (glu_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
