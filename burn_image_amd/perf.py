@@ -210,7 +210,7 @@ def bench_block(a) -> dict:
 
 def bench_copy(a) -> dict:
     dev = torch.device("cuda:0")
-    n = a.mib << 20
+    n = (a.kib << 10) if a.kib else (a.mib << 20)
     src = torch.ones(n // 4, dtype=torch.int32, device=dev)
     dst = torch.empty_like(src)
     us = _time(lambda i: dst.copy_(src), a.iters, a.warmup)
@@ -255,6 +255,7 @@ def main(argv=None):
     p.add_argument("--S", type=int, default=4608)
     p = sub.add_parser("copy")
     p.add_argument("--mib", type=int, default=512)
+    p.add_argument("--kib", type=int, default=0, help="size in KiB instead (a launch-cost floor)")
     for p in sub.choices.values():
         p.add_argument("--iters", type=int, default=50)
         p.add_argument("--warmup", type=int, default=5)
