@@ -648,10 +648,13 @@ int q4_gemv_launch(hipStream_t s, const void *x, int x_dtype, int64_t M, int64_t
     // 8 waves per slab measured best (over 12 and 16: more units per wave to pipeline)
     const int64_t pref = max_wps < 8 ? max_wps : 8;
     int64_t wps = kunits >= pref ? pref : ((kunits + 3) / 4) * 4;
-    if (const char *e = std::getenv("BIQ_GEMV_WPS")) {  // tuning: 4, 8, 12 or 16 waves per slab
-      const int64_t v = std::atoll(e);
-      if ((v == 4 || v == 8 || v == 12 || v == 16) && v <= max_wps) wps = v;
-    }
+    // BIQ_GEMV_WPS (tuning): 4, 8, 12 or 16 waves per slab, read once per process
+    static const int64_t forced_wps = [] {
+      const char *e = std::getenv("BIQ_GEMV_WPS");
+      return e ? (int64_t)std::atoll(e) : (int64_t)0;
+    }();
+    if ((forced_wps == 4 || forced_wps == 8 || forced_wps == 12 || forced_wps == 16) && forced_wps <= max_wps)
+      wps = forced_wps;
     const int64_t red_bytes = wps * (fold ? 2 * M : M) * KN_SLAB * 4;
     const int64_t lds = xs_bytes > red_bytes ? xs_bytes : red_bytes;
     if (lds <= 160 * 1024 && nslabs <= 0x7fffffffLL) {
