@@ -533,13 +533,17 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   };
 
   // Pipeline, PF register sets deep: while tile t computes from one LDS buffer, register set
-  // t % PF holds tile t+1 (stored into the other LDS buffer at the start of iteration t, its
-  // conversion overlapping the first LDS reads of tile t) and is then refilled with tile t+1+PF,
-  // so every global load has PF whole tiles to arrive.  Iterations go in pairs so that every set is named at compile time: a loaded
-  // register is never copied while its load is in flight (a copy would make the wave wait for
-  // it).  Two sets where the registers allow it without spilling in the loop, else one.  The
-  // block scales travel in the same sets.
+  // t % PF holds tile t+1 (stored into the other LDS buffer during iteration t) and is then
+  // refilled with tile t+1+PF, so every global load has PF whole tiles to arrive.  Iterations go
+  // in pairs so that every set is named at compile time: a loaded register is never copied while
+  // its load is in flight (a copy would make the wave wait for it).  Two sets where the registers
+  // allow it without spilling in the loop, else one.  The block scales travel in the same sets.
+  // 16-bit activations are stored (converted) after the tile's MFMAs and the refill follows:
+  // stored first, the conversion ran as one VALU burst ahead of the tile's first MFMA, in step on
+  // both waves of a SIMD (measured: -1 to -2% time on the 4608-row shapes, -2% fused SwiGLU).
+  // f32 activations keep the store first: their two hi/lo planes stored late ran +28% slower.
   constexpr int PF = PF_SETS<G, LAYOUT, XMODE, BLK>;
+  constexpr bool STAGE_LATE = XMODE != XM_F32;
   constexpr int NTT = (PF == 2 || TPB == 2) ? 2 : 1;  // K tiles per loop iteration
   TileRegs<G, XMODE, TILE_BLOCKS> RS[PF];
   float sc_hold[WN][TILE_BLOCKS];  // scales of the tile computed next, copied out of its set
@@ -585,12 +589,15 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
       // here makes the compiler merge the freshly loaded registers at the join, which waits for
       // the whole prefetch before the first MFMA.)  The set's scales are copied out after the
       // store, which has waited for the set anyway.
-      store_tile(R, buf ^ 1);
+      auto stage_next = [&]() {
+        store_tile(R, buf ^ 1);
 #pragma unroll
-      for (int j = 0; j < WN; ++j)
+        for (int j = 0; j < WN; ++j)
 #pragma unroll
-        for (int t = 0; t < TILE_BLOCKS; ++t) sc_hold[j][t] = R.sc[j][t];
-      load_tile(kt + (1 + PF) * BK, R);
+          for (int t = 0; t < TILE_BLOCKS; ++t) sc_hold[j][t] = R.sc[j][t];
+        load_tile(kt + (1 + PF) * BK, R);
+      };
+      if constexpr (!STAGE_LATE) stage_next();
 #pragma unroll
       for (int j = 0; j < WN; ++j) b_cur[j] = unpack_q4_f16(w_cur[j]);
 
@@ -668,6 +675,16 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
           for (int i = 0; i < WM; ++i)
 #pragma unroll
             for (int x = 0; x < NSPLIT; ++x) a_cur[i][x] = a_nxt[i][x];
+        }
+      }
+      if constexpr (STAGE_LATE) stage_next();
+      if constexpr (RESC) {
+        // One MFMA, then six VALU, through the tile: otherwise the block-boundary rescale (one
+        // multiply per accumulator) runs as a burst before the block's first MFMA.
+#pragma unroll
+        for (int g = 0; g < BK / 16 * WM * WN; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
         }
       }
       __syncthreads();
