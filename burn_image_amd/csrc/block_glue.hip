@@ -137,6 +137,9 @@ __global__ void __launch_bounds__(GT) block_glue_kernel(GlueArgs a) {
 // block_glue_kernel; only the f32 summation order of the two row sums differs.
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int GR_MAXK = 4;  // vectors of 4 per thread: rows up to 256 * 4 * 4 = 4096 elements
+// The kernel is instantiated per vector count GK = ceil(W / 1024): a 3072-wide row holds 3 vectors
+// per thread in 92 registers (5 waves per SIMD) where the 4-vector form took 137-140 (3 waves);
+// measured on the 4608 x 3072 middle pass: 57 -> 48 us.
 
 template <int DT>
 __device__ __forceinline__ f32x4_t load4(const void *p, int64_t v) {  // elements 4v .. 4v + 3
@@ -170,7 +173,7 @@ __device__ __forceinline__ void store4(void *p, int64_t v, const f32x4_t &x) {
   }
 }
 
-template <int BDT, int NDT>  // branch dtype; next dtype (-1: no next output)
+template <int BDT, int NDT, int GK>  // branch dtype; next dtype (-1: no next output); vectors per thread
 __global__ void __launch_bounds__(GT) block_glue_row_kernel(GlueArgs a) {
   __shared__ float red[GT / 64];
   const int64_t row = blockIdx.x;
@@ -181,9 +184,9 @@ __global__ void __launch_bounds__(GT) block_glue_row_kernel(GlueArgs a) {
   auto row4 = [](const float *p, int64_t v) { return reinterpret_cast<const f32x4_t *>(p)[v]; };
   const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
 
-  f32x4_t u[GR_MAXK], xr[GR_MAXK];  // the modulated branch (then r) and the residual input
+  f32x4_t u[GK], xr[GK];  // the modulated branch (then r) and the residual input
 #pragma unroll
-  for (int k = 0; k < GR_MAXK; ++k) {
+  for (int k = 0; k < GK; ++k) {
     const int64_t v = threadIdx.x + GT * k;
     const bool in = v < nv;
     u[k] = in ? load4<BDT>(a.branch, rv + v) : z;
@@ -191,7 +194,7 @@ __global__ void __launch_bounds__(GT) block_glue_row_kernel(GlueArgs a) {
   }
   float ss = 0.0f;
 #pragma unroll
-  for (int k = 0; k < GR_MAXK; ++k) {
+  for (int k = 0; k < GK; ++k) {
     const int64_t v = threadIdx.x + GT * k;
     if (v < nv) {
       if (a.branch_scale) u[k] *= row4(a.branch_scale, bv + v) + 1.0f;
@@ -204,7 +207,7 @@ __global__ void __launch_bounds__(GT) block_glue_row_kernel(GlueArgs a) {
     const float rms_b = sqrtf(block_sum(ss, red) * inv_w + a.branch_eps);
     ss_r = 0.0f;
 #pragma unroll
-    for (int k = 0; k < GR_MAXK; ++k) {
+    for (int k = 0; k < GK; ++k) {
       const int64_t v = threadIdx.x + GT * k;
       if (v < nv) {
         f32x4_t nb = u[k] / rms_b;
@@ -223,7 +226,7 @@ __global__ void __launch_bounds__(GT) block_glue_row_kernel(GlueArgs a) {
   if constexpr (NDT >= 0) {
     const float rms_r = sqrtf(block_sum(ss_r, red) * inv_w + a.next_eps);
 #pragma unroll
-    for (int k = 0; k < GR_MAXK; ++k) {
+    for (int k = 0; k < GK; ++k) {
       const int64_t v = threadIdx.x + GT * k;
       if (v < nv) {
         f32x4_t n = u[k] / rms_r;
@@ -268,7 +271,14 @@ extern "C" int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t
                    (!next_out || (next_dtype == BIQ_DTYPE_F32 ? al16(next_out) : al8(next_out)));
   if (vec) {
     const dim3 grid((unsigned)rows);
-#define BIQ_GLUE(BD, ND) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND>), grid, dim3(GT), 0, s, a)
+    const int gk = (int)((width / 4 + GT - 1) / GT);
+#define BIQ_GLUE(BD, ND)                                                                           \
+  do {                                                                                             \
+    if (gk == 1) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 1>), grid, dim3(GT), 0, s, a);  \
+    else if (gk == 2) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 2>), grid, dim3(GT), 0, s, a); \
+    else if (gk == 3) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 3>), grid, dim3(GT), 0, s, a); \
+    else hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 4>), grid, dim3(GT), 0, s, a);          \
+  } while (0)
 #define BIQ_GLUE_N(BD)                                                                             \
   do {                                                                                             \
     if (!next_out) BIQ_GLUE(BD, -1);                                                               \

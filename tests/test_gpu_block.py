@@ -36,11 +36,12 @@ def glue_ref(oracle, x, branch, g_b, eps_b, gate, g_n, eps_n, scale, S):
     return r.astype(np.float32), (None if nxt is None else nxt.astype(np.float32))
 
 
-@pytest.mark.parametrize("Wd", [520, 3072, 522, 4100])
+@pytest.mark.parametrize("Wd", [520, 1600, 3072, 4096, 522, 4100])
 def test_gpu_block_glue_residual_and_modulation(gpu, oracle, Wd):
-    """Rows of <= 4096 elements in whole 4-vectors take the wave-per-row kernel (520: the last
-    vectors of a row are held by some lanes only; 3072: the block width); 522 (not whole vectors)
-    and 4100 (wider than a wave's registers) take the workgroup-per-row kernel."""
+    """Rows of <= 4096 elements in whole 4-vectors take the row-in-registers kernel, instantiated
+    per vectors per thread (520: 1, the last vectors of a row held by some threads only; 1600: 2;
+    3072, the block width: 3; 4096: 4); 522 (not whole vectors) and 4100 (wider than the
+    registers hold) take the workgroup-per-row kernel."""
     rng = np.random.default_rng(40)
     Bn, S = 2, 33
     x = rng.standard_normal((Bn, S, Wd)).astype(np.float32)
