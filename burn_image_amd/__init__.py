@@ -8,7 +8,7 @@ from .attention import (F16_STORAGE_F32_ACCUM, STRICT_F32, AttentionKernel, burn
                         NativeQ4FlashAttention, RmsNorm, attention,
                         effective_portable_query_chunk_size, qk_norm_rope)
 from .block import (DoubleStreamAttention, DoubleStreamBlock, GqaAttention, RmsNormZero,
-                    SingleStreamBlock, block_glue)
+                    SingleStreamBlock, block_glue, project_qkv_norm_rope)
 from .linear import (Linear, LuminaFeedForward, linear_forward, q_matmul, q_matmul_swiglu,
                      qwen_linear_forward)
 from .qwen import Qwen3VlTextAttention
@@ -28,7 +28,7 @@ __all__ = [
     "qwen_linear_forward", "Q4Weight", "from_packed", "from_payload", "payload_layout", "split_payload",
     "q4s_storage_block_and_axis", "q4s_stored_dtype", "quantize_q4s_block128_f32",
     "quantize_row_layout_q4s_block_up_to128_f32", "BiqError", "InvalidArgument", "Unsupported",
-    "block_glue", "RmsNormZero", "GqaAttention", "SingleStreamBlock", "DoubleStreamAttention",
+    "block_glue", "project_qkv_norm_rope", "RmsNormZero", "GqaAttention", "SingleStreamBlock", "DoubleStreamAttention",
     "DoubleStreamBlock", "Qwen3VlTextAttention",
     "version", "BOOGU_DENOISER", "QWEN3_VL", "FLUX_VAE", "Q4_KN_AXIS1", "Q4_NK_AXIS0",
 ]

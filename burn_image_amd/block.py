@@ -91,6 +91,57 @@ class RmsNormZero:
                      modulation_rows(self.linear, conditioning, width, 4))
 
 
+def project_qkv_norm_rope(qkv: Linear, tokens: torch.Tensor, norm_q: RmsNorm, norm_k: RmsNorm,
+                          rope: Tuple[torch.Tensor, torch.Tensor], heads: int, kv_heads: int,
+                          head_dim: int, out_dtype: torch.dtype = torch.float16,
+                          stream: Optional[int] = None):
+    """One libbiq launch for self attention's inputs (biq_q4_linear_qk_norm_rope): tokens
+    [B, S, K] times the packed q | k | v weight, then strict-F32 RMSNorm + interleaved RoPE of the
+    q and k heads and the cast of all three, from the projection tile in registers.  The same
+    results as linear_forward(qkv) followed by qk_norm_rope (attention.rs:700-833 with the
+    native_flash.rs:395-583 preparation) within one rounding of ``out_dtype``.  Returns contiguous
+    q [B, S, heads, D], k / v [B, S, kv_heads, D]; raises Unsupported where the fused launch does
+    not apply (head width other than 128, f32 tokens, blocks below 32, a bias)."""
+    w = qkv.weight
+    if qkv.bias is not None:
+        raise _lib.Unsupported(_lib.ERR_UNSUPPORTED, "fused q/k/v projection takes a bias-free weight")
+    if w.layout != _lib.Q4_KN_AXIS1:
+        raise _lib.Unsupported(_lib.ERR_UNSUPPORTED, "fused q/k/v projection takes the [K/8, N] layout")
+    if tokens.dim() != 3 or tokens.dtype not in _DTYPE_CODE:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "fused q/k/v projection takes [B, S, K] tokens")
+    B, S, K = tokens.shape
+    if w.K != K or w.N != (heads + 2 * kv_heads) * head_dim:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "fused q/k/v weight shape mismatch")
+    cos, sin = rope
+    if cos.dim() != 3 or tuple(cos.shape[1:]) != (S, head_dim) or cos.shape != sin.shape:
+        raise _lib.InvalidArgument(_lib.ERR_INVALID_ARG, "fused RoPE tables must be [1|B, S, D]")
+    x = tokens.reshape(B * S, K)
+    if x.stride(-1) != 1 or (x.shape[0] > 1 and x.stride(0) < K):
+        x = x.contiguous()
+    ldx = x.stride(0) if x.shape[0] > 1 else K
+    gq = norm_q.gamma.to(torch.float32).contiguous()
+    gk = norm_k.gamma.to(torch.float32).contiguous()
+    cs = cos.to(torch.float32).contiguous()
+    sn = sin.to(torch.float32).contiguous()
+    q = torch.empty((B, S, heads, head_dim), dtype=out_dtype, device=tokens.device)
+    k = torch.empty((B, S, kv_heads, head_dim), dtype=out_dtype, device=tokens.device)
+    v = torch.empty((B, S, kv_heads, head_dim), dtype=out_dtype, device=tokens.device)
+    st = torch.cuda.current_stream(tokens.device).cuda_stream if stream is None else stream
+    _lib.check(_lib.load().biq_q4_linear_qk_norm_rope(
+        st, x.data_ptr(), _DTYPE_CODE[x.dtype], B, S, K, ldx, w.words.data_ptr(), w.scales.data_ptr(),
+        w.block, heads, kv_heads, head_dim, gq.data_ptr(), gk.data_ptr(), norm_q.epsilon,
+        norm_k.epsilon, cs.data_ptr(), sn.data_ptr(), cs.shape[0], _DTYPE_CODE[out_dtype],
+        q.data_ptr(), k.data_ptr(), v.data_ptr()))
+    return q, k, v
+
+
+def _fused_qkv_applies(qkv: Linear, tokens: torch.Tensor, head_dim: int) -> bool:
+    """The conditions under which biq_q4_linear_qk_norm_rope accepts the call."""
+    w = qkv.weight
+    return (qkv.bias is None and w.layout == _lib.Q4_KN_AXIS1 and w.block >= 32 and head_dim == 128
+            and tokens.dtype in (torch.float16, torch.bfloat16) and tokens.dim() == 3)
+
+
 @dataclass
 class GqaAttention:
     """attention.rs:700-833: bias-free to_q / to_k / to_v / to_out projections, per-head
@@ -119,6 +170,14 @@ class GqaAttention:
         B, Sq, _ = query_tokens.shape
         Sk = key_value_tokens.shape[1]
         H, Hkv, D = self.heads, self.kv_heads, self.head_dim
+        if (self.qkv is not None and query_tokens is key_value_tokens and rope is not None
+                and _fused_qkv_applies(self.qkv, query_tokens, D)):
+            # projection and Q/K preparation in one launch (the f32 projection is never stored)
+            q, k, v = project_qkv_norm_rope(self.qkv, query_tokens, self.norm_q, self.norm_k, rope,
+                                            H, Hkv, D)
+            out = NativeQ4FlashAttention.execute_gqa(q, k, v, self.query_chunk_size,
+                                                     out_dtype=out_dtype or torch.float32)
+            return linear_forward(self.to_out, out.reshape(B, Sq, self.heads * self.head_dim))
         if self.qkv is not None and query_tokens is key_value_tokens:
             fused = linear_forward(self.qkv, query_tokens).view(B, Sq, H + 2 * Hkv, D)
             q, k, v = fused[:, :, :H], fused[:, :, H:H + Hkv], fused[:, :, H + Hkv:]

@@ -232,6 +232,155 @@ __device__ __forceinline__ void store_tile_out(const floatx16_t (&acc)[G::WM][G:
   }
 }
 
+// Fused self-attention projection epilogue (biq_q4_linear_qk_norm_rope).  The output columns are
+// Hq + 2 Hkv heads of 128 (q heads, then k heads, then v heads); a 256 x 256 workgroup tile holds
+// two whole heads.  Per (token, q or k head), in the order of the fused preparation kernel for
+// f32 input (qk_prep.hip): rms = sqrt(sum x^2 / 128 + eps), n = (x / rms) * gamma (the quotient
+// correctly rounded: q = x * (1 / rms) and one residual step, Markstein), interleaved RoPE
+// y_2p = n_2p cos - n_2p+1 sin, y_2p+1 = n_2p+1 cos + n_2p sin, each product and sum rounded in
+// f32; then the cast.  v heads are only cast.  Outputs are contiguous [B, S, H, 128].  Only the
+// sum of squares is added in another order than the preparation kernel's.
+struct QkEpi {
+  const float *q_gamma, *k_gamma, *cos, *sin;
+  void *qo, *ko, *vo;
+  int64_t S, Hq, Hkv;
+  int rope_per_batch;  // 1: cos / sin rows per (batch, token) = per output row; 0: per token
+  int out_bf16;
+  float q_eps, k_eps;
+};
+
+// Each MFMA tile row i (32 rows of every wave) passes through LDS as four (row block, head)
+// groups of 32 rows x 128 columns; thread t then owns 16 consecutive columns (t % 8) of one
+// (row, head) of a group: the row's sum of squares is a 16-term sum plus three lane exchanges,
+// RoPE pairs sit in one thread, and cos / sin / gamma / outputs move as 16-byte vectors.  Waves
+// 0-3 take the tile's first head and waves 4-7 its second, in both passes of every i.
+constexpr int QK_LD = 132;  // LDS row stride of a group, in floats
+template <class G>
+__device__ __forceinline__ void qk_epilogue(const floatx16_t (&acc)[G::WM][G::WN], int64_t m0,
+                                            int64_t n0, int64_t M, const QkEpi &e,
+                                            float *__restrict__ lds) {
+#pragma clang fp contract(off)
+  static_assert(G::WM == 4 && G::WN == 2 && G::WAVES_M == 2 && G::WAVES_N == 4 && G::NTHREADS == 512,
+                "two 128-column heads per 256 x 256 tile");
+  constexpr int D = 128;
+  constexpr uint32_t OOB = 0x80000000u;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
+  const int l32 = lane & 31, lh = lane >> 5;
+  // writer side: this wave's 32 x 64 piece of group (wm, wn / 2) at columns (wn % 2) * 64
+  float *wr = lds + (wm * 2 + (wn >> 1)) * 32 * QK_LD + (wn & 1) * 64 + l32;
+  // reader side: head hh of the tile, chunk k (columns 16 k .. 16 k + 15)
+  const int hh = wave >> 2, k = tid & 7;
+  const int64_t head = n0 / D + hh;  // wave-uniform
+  const int64_t Hq = e.Hq, Hkv = e.Hkv;
+  const int kind = head < Hq ? 0 : (head < Hq + Hkv ? 1 : (head < Hq + 2 * Hkv ? 2 : 3));
+  const int64_t H = kind == 0 ? Hq : Hkv;
+  const int64_t hk = head - (kind == 0 ? 0 : (kind == 1 ? Hq : Hq + Hkv));
+  float gm[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) gm[c] = 0.0f;
+  if (kind < 2) {
+    const float4 *gp = reinterpret_cast<const float4 *>((kind == 0 ? e.q_gamma : e.k_gamma) + 16 * k);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 v = gp[c];
+      gm[4 * c] = v.x; gm[4 * c + 1] = v.y; gm[4 * c + 2] = v.z; gm[4 * c + 3] = v.w;
+    }
+  }
+  const float eps = kind == 0 ? e.q_eps : e.k_eps;
+  const uint32_t S = (uint32_t)e.S;
+  auto rsrc = [](const void *base, int64_t bytes) {
+    const uint32_t n = bytes > 0x7fffffffLL ? 0x7fffffffu : (bytes < 0 ? 0u : (uint32_t)bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)n, 0x00020000);
+  };
+  const int64_t table_rows = e.rope_per_batch ? M : e.S;
+  const auto cs_rs = rsrc(e.cos, table_rows * D * 4), sn_rs = rsrc(e.sin, table_rows * D * 4);
+  u32x4_t packed[4][2][2];  // (i, pass): the thread's 16 outputs as 16-bit pairs
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        wr[(8 * (r >> 2) + 4 * lh + (r & 3)) * QK_LD + 32 * j] = acc[i][j][r];
+    __syncthreads();
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      const int rr = (tid >> 3) & 31;                // row of the group
+      const int g = 2 * ps + hh;                     // group: row block ps, head hh
+      const int64_t row = m0 + ps * 128 + 32 * i + rr;
+      float x[16];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float4 v = reinterpret_cast<const float4 *>(lds + (g * 32 + rr) * QK_LD + 16 * k)[c];
+        x[4 * c] = v.x; x[4 * c + 1] = v.y; x[4 * c + 2] = v.z; x[4 * c + 3] = v.w;
+      }
+      float y[16];
+      if (kind < 2) {
+        const uint32_t trow = e.rope_per_batch ? (uint32_t)(row < M ? row : M - 1) : (uint32_t)(row % (int64_t)S);
+        const uint32_t to = (trow * (uint32_t)D + 16u * k) * 4u;
+        float cs[16], sn[16];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(cs_rs, to + 16u * c, 0, 0);
+          const u32x4_t b = __builtin_amdgcn_raw_buffer_load_b128(sn_rs, to + 16u * c, 0, 0);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            cs[4 * c + t] = biq::bitcast<float>(a[t]);
+            sn[4 * c + t] = biq::bitcast<float>(b[t]);
+          }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) ss = ss + x[c] * x[c];
+        // the eight threads of the row add their sums pairwise: every one ends with the same total
+        ss = ss + __shfl_xor(ss, 1);
+        ss = ss + __shfl_xor(ss, 2);
+        ss = ss + __shfl_xor(ss, 4);
+        const float rms = sqrtf(ss / (float)D + eps);
+        const float inv = 1.0f / rms;
+        float n[16];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+          const float q = x[c] * inv;
+          n[c] = __builtin_fmaf(__builtin_fmaf(-q, rms, x[c]), inv, q) * gm[c];
+        }
+#pragma unroll
+        for (int c = 0; c < 16; c += 2) {
+          y[c] = (n[c] * cs[c]) + ((-n[c + 1]) * sn[c]);
+          y[c + 1] = (n[c + 1] * cs[c + 1]) + (n[c] * sn[c + 1]);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 16; ++c) y[c] = x[c];
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t w = e.out_bf16 ? (biq::f32_to_bf16_bits(y[2 * c]) | (biq::f32_to_bf16_bits(y[2 * c + 1]) << 16))
+                                      : biq::pack_f16x2(y[2 * c], y[2 * c + 1]);
+        packed[i][ps][c >> 2][c & 3] = w;
+      }
+    }
+    __syncthreads();  // the next i rewrites the groups
+  }
+  if (kind == 3) return;  // columns past N (the last tile of an odd head count)
+  // stores: (row, head hk) chunk k = 32 bytes; rows past M take an out-of-range offset
+  uint16_t *out = reinterpret_cast<uint16_t *>(kind == 0 ? e.qo : (kind == 1 ? e.ko : e.vo)) + hk * D + 16 * k;
+  const auto out_rs = rsrc(out, (M - 1) * H * D * 2 + 32);  // through the last row's 16 outputs
+  const uint32_t row_bytes = (uint32_t)(H * D * 2);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      const int64_t row = m0 + ps * 128 + 32 * i + ((tid >> 3) & 31);
+      const uint32_t o = row < M ? (uint32_t)row * row_bytes : OOB;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        __builtin_amdgcn_raw_buffer_store_b128(packed[i][ps][h], out_rs, o + 16u * h, 0, 0);
+    }
+}
+
 // Tail reduction.  One thread takes one output register q of four consecutive source threads
 // of one tail tile (one 16-byte load per part, coalesced), adds the `parts` partials in K order
 // and writes the four outputs: same rows and columns, bias and SwiGLU gate as the GEMM epilogue
@@ -282,13 +431,15 @@ __global__ void __launch_bounds__(RED_THREADS)
   }
 }
 
-template <class G, int LAYOUT, int XMODE, int BLK, bool GLU>
+// EPI = 1: the fused Q/K preparation epilogue (qk_epilogue; every tile owned, yv unused).
+template <class G, int LAYOUT, int XMODE, int BLK, bool GLU, int EPI = 0>
 __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     q4_gemm_kernel(const void *__restrict__ xv, int64_t ldx, const uint32_t *__restrict__ words,
                    const float *__restrict__ scales, const uint32_t *__restrict__ words3,
                    const float *__restrict__ scales3, const float *__restrict__ bias,
                    void *__restrict__ yv, int y_dtype, int64_t M, int64_t N, int64_t K,
-                   int tiles_m, int tiles_n, SkPlan sk) {
+                   int tiles_m, int tiles_n, SkPlan sk, QkEpi qe) {
+  static_assert(EPI == 0 || (G::RESCALE && !GLU), "the fused epilogue runs on the 256 x 256 tile");
   constexpr int WM = G::WM, WN = G::WN, BM = G::BM, BN = G::BN, NT = G::NTHREADS;
   static_assert(!GLU || WN == 2, "the SwiGLU form pairs the two column tiles of a wave");
   constexpr int BNO = GLU ? BN / 2 : BN;  // output columns per workgroup
@@ -320,7 +471,9 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
   };
   const int64_t first = tail_wg ? xcd_order(L - sk.dp_tiles, sk.sk_wgs) : xcd_order(L, sk.dp_tiles);
-  const int64_t n_seg = tail_wg ? (chunks - first + sk.sk_wgs - 1) / sk.sk_wgs : 1;
+  // (the fused epilogue's launches own every tile: one segment, known at compile time, so no
+  // value of the segment loop stays live through the epilogue)
+  const int64_t n_seg = EPI == 1 ? 1 : (tail_wg ? (chunks - first + sk.sk_wgs - 1) / sk.sk_wgs : 1);
 
   for (int64_t seg = 0; seg < n_seg; ++seg) {
   const int64_t c = first + seg * sk.sk_wgs;  // tail chunk (tail workgroups only)
@@ -699,6 +852,10 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
 #pragma unroll
       for (int j = 0; j < WN; ++j) acc[i][j] *= t_prev[j];
   }
+  if constexpr (EPI == 1) {  // the loop's last barrier has retired every LDS access
+    qk_epilogue<G>(acc, m0, n0, M, qe, reinterpret_cast<float *>(&As[0][0][0]));
+    continue;
+  }
   if (ku0 == 0 && ku1 == units) {  // the whole K of the tile
     store_tile_out<G, GLU>(acc, m0, n0, bias, yv, y_dtype, M, N);
     continue;
@@ -788,7 +945,7 @@ int launch_geo(hipStream_t s, const void *x, int64_t ldx, const Q4Args &w, const
   dim3 grid((unsigned)(plan.dp_tiles + plan.sk_wgs));
   hipLaunchKernelGGL((q4_gemm_kernel<GG, LAYOUT, XMODE, B, GLU>), grid, dim3(GG::NTHREADS), 0, s, x,
                      ldx, w.words, w.scales, w.words3, w.scales3, bias, y, y_dtype, M, N, K,
-                     tiles_m, tiles_n, plan);
+                     tiles_m, tiles_n, plan, QkEpi{});
   if (plan.sk_wgs > 0) {
     const int st = biq::check_launch(GLU ? "q4 linear swiglu" : "q4 linear");
     if (st != BIQ_OK) return st;
@@ -981,4 +1138,77 @@ extern "C" int biq_q4_linear_swiglu(void *stream, const void *x, int x_dtype, in
   if (layout == BIQ_Q4_KN_AXIS1)
     return launch_layout<BIQ_Q4_KN_AXIS1, true>(s, x_dtype, block, x, ldx, w, nullptr, y, y_dtype, M, N, K, nullptr);
   return launch_layout<BIQ_Q4_NK_AXIS0, true>(s, x_dtype, block, x, ldx, w, nullptr, y, y_dtype, M, N, K, nullptr);
+}
+
+namespace {
+// The fused projection on the 256 x 256 tile, every tile owned (the epilogue needs whole rows of
+// K): one launch.
+template <int XMODE, int B>
+int launch_qk(hipStream_t s, const void *x, int64_t ldx, const uint32_t *words, const float *scales,
+              int64_t M, int64_t N, int64_t K, const QkEpi &e) {
+  using GG = GemmGeoBig;
+  constexpr int64_t UNIT = (int64_t)(B >= GG::BK ? B : GG::BK);
+  const int tiles_m = (int)((M + GG::BM - 1) / GG::BM), tiles_n = (int)((N + GG::BN - 1) / GG::BN);
+  const int64_t T = (int64_t)tiles_m * tiles_n;
+  const SkPlan plan{(int)T, 0, 1, (K + UNIT - 1) / UNIT, nullptr};
+  hipLaunchKernelGGL((q4_gemm_kernel<GG, BIQ_Q4_KN_AXIS1, XMODE, B, false, 1>), dim3((unsigned)T),
+                     dim3(GG::NTHREADS), 0, s, x, ldx, words, scales, nullptr, nullptr, nullptr,
+                     nullptr, 0, M, N, K, tiles_m, tiles_n, plan, e);
+  return biq::check_launch("q4 linear qk norm rope");
+}
+
+template <int XMODE>
+int launch_qk_blk(hipStream_t s, int block, const void *x, int64_t ldx, const uint32_t *words,
+                  const float *scales, int64_t M, int64_t N, int64_t K, const QkEpi &e) {
+  switch (block) {
+    case 32: return launch_qk<XMODE, 32>(s, x, ldx, words, scales, M, N, K, e);
+    case 64: return launch_qk<XMODE, 64>(s, x, ldx, words, scales, M, N, K, e);
+    default: return launch_qk<XMODE, 128>(s, x, ldx, words, scales, M, N, K, e);
+  }
+}
+}  // namespace
+
+extern "C" int biq_q4_linear_qk_norm_rope(void *stream, const void *x, int x_dtype, int64_t B,
+                                          int64_t S, int64_t K, int64_t ldx, const uint32_t *words,
+                                          const float *scales, int block, int64_t Hq, int64_t Hkv,
+                                          int64_t D, const float *q_gamma, const float *k_gamma,
+                                          float q_eps, float k_eps, const float *cos,
+                                          const float *sin, int64_t rope_batch, int out_dtype,
+                                          void *q_out, void *k_out, void *v_out) {
+  biq::clear_error();
+  if (!q_gamma || !k_gamma || !cos || !sin || !q_out || !k_out || !v_out)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "null pointer argument");
+  if (B <= 0 || S <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "fused projection requires non-empty batch, tokens and heads");
+  if (Hq % Hkv != 0)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "GQA query heads must be divisible by key/value heads");
+  if (out_dtype != BIQ_DTYPE_F16 && out_dtype != BIQ_DTYPE_BF16)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "fused preparation output must be F16 or BF16");
+  if (!(q_eps > 0.0f) || !(k_eps > 0.0f) || q_eps == INFINITY || k_eps == INFINITY)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "fused RMSNorm epsilon must be finite and positive");
+  if (rope_batch != 1 && rope_batch != B)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "fused RoPE batch must be one or match the token batch");
+  // the epilogue's buffer offsets are 32-bit: each output and the cos / sin tables must span less
+  // than 2^31 bytes
+  if (B > (1LL << 31) / S || Hq + 2 * Hkv > 32768 || B * S * Hq * D * 2 >= (1LL << 31) ||
+      (rope_batch == B ? B * S : S) * D * 4 >= (1LL << 31))
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "fused projection: outputs or RoPE tables of 2 GiB or more");
+  auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (!al16(q_gamma) || !al16(k_gamma) || !al16(cos) || !al16(sin) || !al16(q_out) || !al16(k_out) ||
+      !al16(v_out))
+    return biq::fail(BIQ_ERR_INVALID_ARG, "fused projection: gamma, RoPE tables and outputs must be 16-byte aligned");
+  const int64_t M = B * S, N = (Hq + 2 * Hkv) * D;
+  const int st = check_linear(x, x_dtype, M, K, ldx, words, scales, BIQ_Q4_KN_AXIS1, block, N, q_out,
+                             out_dtype);
+  if (st != BIQ_OK) return st;
+  if (D != 128)
+    return biq::fail(BIQ_ERR_UNSUPPORTED, "fused projection + Q/K preparation needs 128-wide heads");
+  if (x_dtype == BIQ_DTYPE_F32 || block < 32)
+    return biq::fail(BIQ_ERR_UNSUPPORTED,
+                     "fused projection + Q/K preparation needs 16-bit activations and blocks of at least 32");
+  const QkEpi e{q_gamma, k_gamma, cos, sin, q_out, k_out, v_out, S, Hq, Hkv, rope_batch == B && B > 1 ? 1 : 0,
+                out_dtype == BIQ_DTYPE_BF16 ? 1 : 0, q_eps, k_eps};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (x_dtype == BIQ_DTYPE_BF16) return launch_qk_blk<XM_BF16>(s, block, x, ldx, words, scales, M, N, K, e);
+  return launch_qk_blk<XM_F16>(s, block, x, ldx, words, scales, M, N, K, e);
 }

@@ -274,6 +274,29 @@ int biq_qk_norm_rope(void *stream, const void *q, const void *k, const void *v, 
                      int64_t rope_batch, int rope_layout, int out_dtype, void *q_out, void *k_out,
                      void *v_out);
 
+/* Fused self-attention input: the packed-Q4 projection of the token rows onto q | k | v heads
+ * followed by the preparation biq_qk_norm_rope does (BIQ_ROPE_INTERLEAVED, f32 projections), in
+ * one launch whose epilogue normalises, rotates and casts the projection tile in registers: the
+ * f32 projection is never written.  Replaces, for GqaAttention's self attention with one packed
+ * [K, (Hq + 2 Hkv) * D] weight (crates/burn_boogu/src/model/attention.rs:700-833: to_q / to_k /
+ * to_v, then prepare_gqa_strict_norm_rope_padded_qkv_kernel, native_flash.rs:395-583), the pair
+ * biq_q4_linear + biq_qk_norm_rope.  x: [B * S, K] rows (row stride ldx) in F16 or BF16; the
+ * weight in BIQ_Q4_KN_AXIS1 with block 32, 64 or 128; q_gamma / k_gamma [D] f32; cos / sin
+ * [rope_batch, S, D] f32 (rope_batch 1 or B); outputs contiguous q_out [B, S, Hq, D], k_out /
+ * v_out [B, S, Hkv, D] in out_dtype (F16 or BF16).  Arithmetic: the projection as biq_q4_linear
+ * (every tile over the whole K, running block-scale rescale), then per row and head the
+ * preparation's f32 steps; only the f32 sum of squares is added in another order, so results
+ * equal the two-call path within one rounding of the output type.  D must be 128 and the other
+ * requirements as biq_q4_linear, else BIQ_ERR_UNSUPPORTED (callers then make the two calls).
+ * No scratch. */
+int biq_q4_linear_qk_norm_rope(void *stream, const void *x, int x_dtype, int64_t B, int64_t S,
+                               int64_t K, int64_t ldx, const uint32_t *words, const float *scales,
+                               int block, int64_t Hq, int64_t Hkv, int64_t D,
+                               const float *q_gamma, const float *k_gamma, float q_eps,
+                               float k_eps, const float *cos, const float *sin,
+                               int64_t rope_batch, int out_dtype, void *q_out, void *k_out,
+                               void *v_out);
+
 #ifdef __cplusplus
 }
 #endif
