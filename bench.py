@@ -7,7 +7,8 @@ attention (B1 H24 S4608 D128, bf16 Q/K/V, f32 output).  Prints one JSON line.  A
 steps it also times, as extra keys:
   * the fused SwiGLU projection (both 3072x12288 up weights in one pass);
   * the whole modulated denoise block (SingleStreamBlock.forward: modulation GEMV, three glue
-    passes, fused QKV projection, Q/K norm + RoPE, attention, O, fused SwiGLU, down) at
+    passes, the QKV projection with the Q/K norm + RoPE epilogue, attention, O, fused SwiGLU,
+    down) at
     4608 tokens x hidden 3072, 24 heads of 128, SwiGLU 12288, bf16 activations
     (`ms_per_denoise_block`), next to the sum of its GEMM and attention kernels;
   * the small-M route (one modulation row, 1 x 3072 x 12288, and 16 x 3072 x 9216) in GB/s over
@@ -142,7 +143,8 @@ def cpu_baseline(args, words_np, scales_np, x_np, q_np, k_np, v_np):
 
 def time_denoise_block(B, W, dev, weights, w3, args):
     """SingleStreamBlock.forward (block.rs:84-134) at 4608 x 3072: modulation GEMV, three glue
-    passes, fused QKV, Q/K norm + RoPE, attention, O, fused SwiGLU, down; bf16 activations.
+    passes, the QKV projection with the Q/K norm + RoPE epilogue, attention, O, fused SwiGLU,
+    down; bf16 activations.
     Returns the mean ms per forward (events around each call)."""
     import torch
     from burn_image_amd import block as BL
@@ -399,7 +401,7 @@ def main():
         "frac_peak": round(step_flops / (ms_per_step * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "ms_per_denoise_block": round(block_measured_ms, 4),
         "denoise_block": ("SingleStreamBlock.forward measured end to end (events): modulation GEMV, "
-                          "3 glue passes, fused QKV, Q/K norm+RoPE, attention, O, fused SwiGLU, down; "
+                          "3 glue passes, QKV projection with the Q/K norm+RoPE epilogue, attention, O, fused SwiGLU, down; "
                           "4608 tok x 3072, 24x128 heads, SwiGLU 12288, bf16 activations"),
         "denoise_block_tflops": round(1.652e12 / (block_measured_ms * 1e-3) / 1e12, 2),
         "ms_sum_block_kernels": round(block_ms, 4),
