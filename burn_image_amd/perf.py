@@ -6,6 +6,7 @@
                                             [--causal] [--segments 1024:64:512]
     python -m burn_image_amd.perf qk_prep --S 4608 --Hq 24 --Hkv 24 --D 128 [--dtype f32]
     python -m burn_image_amd.perf glue --S 4608 --W 3072 [--dtype bf16]
+    python -m burn_image_amd.perf qkv_prep --S 4608 [--Hq 24 --Hkv 24]
     python -m burn_image_amd.perf block --S 4608   (SingleStreamBlock.forward, 3072 wide)
     python -m burn_image_amd.perf copy --mib 512   (a plain device copy of known size: the
                                                     calibration kernel for HBM byte counters)
@@ -177,8 +178,9 @@ def bench_glue(a) -> dict:
 
 def bench_block(a) -> dict:
     """SingleStreamBlock.forward (block.rs:84-134) at S tokens x 3072, 24 x 128 heads, SwiGLU
-    12288, bf16 activations, random packed weights: modulation GEMV, three glue passes, fused
-    QKV, Q/K norm + RoPE, attention, O, fused SwiGLU, down (eager launches, as a caller runs it)."""
+    12288, bf16 activations, random packed weights: modulation GEMV, three glue passes, the QKV
+    projection with the Q/K norm + RoPE epilogue, attention, O, fused SwiGLU, down (eager launches,
+    as a caller runs it)."""
     from . import block as BL
     from . import linear as LN
     from . import rope as R
@@ -206,6 +208,36 @@ def bench_block(a) -> dict:
     cond = torch.randn((1, C), device=dev, generator=g)
     us = _time(lambda i: blk.forward(tokens, rope, cond), a.iters, a.warmup)
     return {"op": "block", "S": a.S, "hidden": Wd, "heads": H, "head_dim": D, "ffn": F, "us": round(us, 3)}
+
+
+def bench_qkv_prep(a) -> dict:
+    """The fused self-attention input launch (biq_q4_linear_qk_norm_rope): tokens [1, S, 3072]
+    bf16 times a packed q | k | v weight (block 128) with the Q/K RMSNorm + RoPE + f16 cast in the
+    epilogue.  GB/s counts the algorithmic bytes: activations, words, scales, cos / sin tables
+    read once, f16 Q / K / V written."""
+    from . import block as BL
+    from . import linear as LN
+    from . import rope as R
+    from .workloads import boogu_joint_ids
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    Wd, H, Hkv, D = 3072, a.Hq, a.Hkv, 128
+    N = (H + 2 * Hkv) * D
+    words = torch.randint(-2 ** 31, 2 ** 31 - 1, (Wd // 8, N), dtype=torch.int32, device=dev, generator=g)
+    scales = torch.rand((Wd // 128, N), device=dev, generator=g) * 0.015 + 0.005
+    w = LN.Linear(from_packed(words, scales, 1, 128, (Wd, N)))
+    ids = boogu_joint_ids(2)[: a.S]
+    cos, sin = R.rope_values(ids, [32, 48, 48], 1.0e4)
+    rope = (torch.from_numpy(cos[None]).to(dev), torch.from_numpy(sin[None]).to(dev))
+    x = torch.randn((1, a.S, Wd), device=dev, generator=g).to(torch.bfloat16)
+    n = RmsNorm(torch.ones(D, device=dev))
+    us = _time(lambda i: BL.project_qkv_norm_rope(w, x, n, n, rope, H, Hkv, D), a.iters, a.warmup)
+    flops = 2.0 * a.S * Wd * N
+    nbytes = a.S * Wd * 2 + Wd * N // 2 + (Wd // 128) * N * 4 + 2 * a.S * D * 4 + a.S * N * 2
+    return {"op": "qkv_prep", "S": a.S, "K": Wd, "N": N, "us": round(us, 3),
+            "tflops": round(flops / (us * 1e-6) / 1e12, 2),
+            "frac_mfma_peak": round(flops / (us * 1e-6) / 1e12 / 2500.0, 4),
+            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
 
 
 def bench_copy(a) -> dict:
@@ -253,6 +285,10 @@ def main(argv=None):
     p.add_argument("--dtype", default="bf16", choices=list(DT))
     p = sub.add_parser("block")
     p.add_argument("--S", type=int, default=4608)
+    p = sub.add_parser("qkv_prep")
+    p.add_argument("--S", type=int, default=4608)
+    p.add_argument("--Hq", type=int, default=24)
+    p.add_argument("--Hkv", type=int, default=24)
     p = sub.add_parser("copy")
     p.add_argument("--mib", type=int, default=512)
     p.add_argument("--kib", type=int, default=0, help="size in KiB instead (a launch-cost floor)")
@@ -265,7 +301,8 @@ def main(argv=None):
     _GRAPH = a.graph
     _lib.load()
     fn = {"q4_linear": bench_q4_linear, "attention": bench_attention, "qk_prep": bench_qk_prep,
-          "glue": bench_glue, "block": bench_block, "copy": bench_copy}[a.op]
+          "glue": bench_glue, "block": bench_block, "qkv_prep": bench_qkv_prep,
+          "copy": bench_copy}[a.op]
     print(json.dumps(fn(a)), flush=True)
 
 
