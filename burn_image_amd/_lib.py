@@ -53,7 +53,7 @@ SIGNATURES = {
     "biq_q4_linear_noalloc": ([_P, _P, _I, _I64, _I64, _I64, _P, _P, _I, _I, _I64, _P, _P, _I], _I),
     "biq_q4_linear_swiglu": ([_P, _P, _I, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I, _I64, _P, _I], _I),
     "biq_q4_linear_qk_norm_rope": ([_P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _I64,
-                                    _P, _P, ctypes.c_float, ctypes.c_float, _P, _P, _I64, _I,
+                                    _P, _P, ctypes.c_float, ctypes.c_float, _P, _P, _I64, _I, _I,
                                     _P, _P, _P], _I),
     "biq_attention": ([_P, _P, _P, _P, _P, _I, _I, _I64, _I64, _I64, _I64, _I64, _I64,
                        ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I64),

@@ -238,14 +238,16 @@ __device__ __forceinline__ void store_tile_out(const floatx16_t (&acc)[G::WM][G:
 // f32 input (qk_prep.hip): rms = sqrt(sum x^2 / 128 + eps), n = (x / rms) * gamma (the quotient
 // correctly rounded: q = x * (1 / rms) and one residual step, Markstein), interleaved RoPE
 // y_2p = n_2p cos - n_2p+1 sin, y_2p+1 = n_2p+1 cos + n_2p sin, each product and sum rounded in
-// f32; then the cast.  v heads are only cast.  Outputs are contiguous [B, S, H, 128].  Only the
-// sum of squares is added in another order than the preparation kernel's.
+// f32; then the cast.  v heads are only cast.  Outputs are contiguous [B, S, H, 128] or
+// [B, H, S, 128].  Only the sum of squares is added in another order than the preparation
+// kernel's.
 struct QkEpi {
   const float *q_gamma, *k_gamma, *cos, *sin;
   void *qo, *ko, *vo;
   int64_t S, Hq, Hkv;
   int rope_per_batch;  // 1: cos / sin rows per (batch, token) = per output row; 0: per token
   int out_bf16;
+  int head_major;      // outputs [B, H, S, 128] instead of [B, S, H, 128]
   float q_eps, k_eps;
 };
 
@@ -365,16 +367,24 @@ __device__ __forceinline__ void qk_epilogue(const floatx16_t (&acc)[G::WM][G::WN
     __syncthreads();  // the next i rewrites the groups
   }
   if (kind == 3) return;  // columns past N (the last tile of an odd head count)
-  // stores: (row, head hk) chunk k = 32 bytes; rows past M take an out-of-range offset
-  uint16_t *out = reinterpret_cast<uint16_t *>(kind == 0 ? e.qo : (kind == 1 ? e.ko : e.vo)) + hk * D + 16 * k;
-  const auto out_rs = rsrc(out, (M - 1) * H * D * 2 + 32);  // through the last row's 16 outputs
-  const uint32_t row_bytes = (uint32_t)(H * D * 2);
+  // stores: (row, head hk) chunk k = 32 bytes; rows past M take an out-of-range offset.  Element
+  // (row = b S + s, hk, d) sits at (row H + hk) D + d, or head-major at ((b H + hk) S + s) D + d
+  // = (row + b (H - 1) S + hk S) D + d.
+  uint16_t *out = reinterpret_cast<uint16_t *>(kind == 0 ? e.qo : (kind == 1 ? e.ko : e.vo)) + 16 * k;
+  const auto out_rs = rsrc(out, (M * H * D - 16 * k) * 2);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int ps = 0; ps < 2; ++ps) {
       const int64_t row = m0 + ps * 128 + 32 * i + ((tid >> 3) & 31);
-      const uint32_t o = row < M ? (uint32_t)row * row_bytes : OOB;
+      uint32_t el;  // element offset of the (row, head) from `out`
+      if (e.head_major) {
+        const uint32_t b = (uint32_t)row / S;
+        el = ((uint32_t)row + b * (uint32_t)((H - 1) * e.S) + (uint32_t)(hk * e.S)) * (uint32_t)D;
+      } else {
+        el = ((uint32_t)row * (uint32_t)H + (uint32_t)hk) * (uint32_t)D;
+      }
+      const uint32_t o = row < M ? el * 2u : OOB;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
         __builtin_amdgcn_raw_buffer_store_b128(packed[i][ps][h], out_rs, o + 16u * h, 0, 0);
@@ -1174,7 +1184,7 @@ extern "C" int biq_q4_linear_qk_norm_rope(void *stream, const void *x, int x_dty
                                           int64_t D, const float *q_gamma, const float *k_gamma,
                                           float q_eps, float k_eps, const float *cos,
                                           const float *sin, int64_t rope_batch, int out_dtype,
-                                          void *q_out, void *k_out, void *v_out) {
+                                          int head_major, void *q_out, void *k_out, void *v_out) {
   biq::clear_error();
   if (!q_gamma || !k_gamma || !cos || !sin || !q_out || !k_out || !v_out)
     return biq::fail(BIQ_ERR_INVALID_ARG, "null pointer argument");
@@ -1188,6 +1198,8 @@ extern "C" int biq_q4_linear_qk_norm_rope(void *stream, const void *x, int x_dty
     return biq::fail(BIQ_ERR_INVALID_ARG, "fused RMSNorm epsilon must be finite and positive");
   if (rope_batch != 1 && rope_batch != B)
     return biq::fail(BIQ_ERR_INVALID_ARG, "fused RoPE batch must be one or match the token batch");
+  if (head_major != 0 && head_major != 1)
+    return biq::fail(BIQ_ERR_INVALID_ARG, "fused projection output layout must be 0 ([B, S, H, D]) or 1 ([B, H, S, D])");
   // the epilogue's buffer offsets are 32-bit: each output and the cos / sin tables must span less
   // than 2^31 bytes
   if (B > (1LL << 31) / S || Hq + 2 * Hkv > 32768 || B * S * Hq * D * 2 >= (1LL << 31) ||
@@ -1207,7 +1219,7 @@ extern "C" int biq_q4_linear_qk_norm_rope(void *stream, const void *x, int x_dty
     return biq::fail(BIQ_ERR_UNSUPPORTED,
                      "fused projection + Q/K preparation needs 16-bit activations and blocks of at least 32");
   const QkEpi e{q_gamma, k_gamma, cos, sin, q_out, k_out, v_out, S, Hq, Hkv, rope_batch == B && B > 1 ? 1 : 0,
-                out_dtype == BIQ_DTYPE_BF16 ? 1 : 0, q_eps, k_eps};
+                out_dtype == BIQ_DTYPE_BF16 ? 1 : 0, head_major, q_eps, k_eps};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (x_dtype == BIQ_DTYPE_BF16) return launch_qk_blk<XM_BF16>(s, block, x, ldx, words, scales, M, N, K, e);
   return launch_qk_blk<XM_F16>(s, block, x, ldx, words, scales, M, N, K, e);

@@ -113,10 +113,16 @@ def bench_attention(a) -> dict:
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(0)
     dt = DT[a.dtype]
-    q = torch.randn((a.B, a.H, a.S, a.D), device=dev, generator=g).to(dt)
-    k = torch.randn((a.B, a.Hkv, a.S, a.D), device=dev, generator=g).to(dt)
-    v = torch.randn((a.B, a.Hkv, a.S, a.D), device=dev, generator=g).to(dt)
-    o = torch.empty((a.B, a.H, a.S, a.D), dtype=DT[a.odtype], device=dev)
+    if a.token_major:  # [B, S, H, D] storage viewed as [B, H, S, D] (the block's GQA layout)
+        q = torch.randn((a.B, a.S, a.H, a.D), device=dev, generator=g).to(dt).permute(0, 2, 1, 3)
+        k = torch.randn((a.B, a.S, a.Hkv, a.D), device=dev, generator=g).to(dt).permute(0, 2, 1, 3)
+        v = torch.randn((a.B, a.S, a.Hkv, a.D), device=dev, generator=g).to(dt).permute(0, 2, 1, 3)
+        o = torch.empty((a.B, a.S, a.H, a.D), dtype=DT[a.odtype], device=dev).permute(0, 2, 1, 3)
+    else:
+        q = torch.randn((a.B, a.H, a.S, a.D), device=dev, generator=g).to(dt)
+        k = torch.randn((a.B, a.Hkv, a.S, a.D), device=dev, generator=g).to(dt)
+        v = torch.randn((a.B, a.Hkv, a.S, a.D), device=dev, generator=g).to(dt)
+        o = torch.empty((a.B, a.H, a.S, a.D), dtype=DT[a.odtype], device=dev)
     cu = None
     pairs = a.S * a.S
     if a.segments:
@@ -273,6 +279,7 @@ def main(argv=None):
     p.add_argument("--odtype", default="f32", choices=list(DT))
     p.add_argument("--causal", action="store_true")
     p.add_argument("--segments", default="", help="total:min:max segment draw (as the C5 workload)")
+    p.add_argument("--token-major", action="store_true", help="Q/K/V/O stored [B, S, H, D]")
     p = sub.add_parser("qk_prep")
     p.add_argument("--S", type=int, default=4608)
     p.add_argument("--Hq", type=int, default=24)

@@ -283,7 +283,9 @@ int biq_qk_norm_rope(void *stream, const void *q, const void *k, const void *v, 
  * biq_q4_linear + biq_qk_norm_rope.  x: [B * S, K] rows (row stride ldx) in F16 or BF16; the
  * weight in BIQ_Q4_KN_AXIS1 with block 32, 64 or 128; q_gamma / k_gamma [D] f32; cos / sin
  * [rope_batch, S, D] f32 (rope_batch 1 or B); outputs contiguous q_out [B, S, Hq, D], k_out /
- * v_out [B, S, Hkv, D] in out_dtype (F16 or BF16).  Arithmetic: the projection as biq_q4_linear
+ * v_out [B, S, Hkv, D] in out_dtype (F16 or BF16), or with head_major = 1 [B, H, S, D] (the
+ * attention kernel reads each head's keys as one contiguous run).  Gamma, tables and outputs
+ * 16-byte aligned; each output and table below 2 GiB.  Arithmetic: the projection as biq_q4_linear
  * (every tile over the whole K, running block-scale rescale), then per row and head the
  * preparation's f32 steps; only the f32 sum of squares is added in another order, so results
  * equal the two-call path within one rounding of the output type.  D must be 128 and the other
@@ -294,8 +296,8 @@ int biq_q4_linear_qk_norm_rope(void *stream, const void *x, int x_dtype, int64_t
                                int block, int64_t Hq, int64_t Hkv, int64_t D,
                                const float *q_gamma, const float *k_gamma, float q_eps,
                                float k_eps, const float *cos, const float *sin,
-                               int64_t rope_batch, int out_dtype, void *q_out, void *k_out,
-                               void *v_out);
+                               int64_t rope_batch, int out_dtype, int head_major, void *q_out,
+                               void *k_out, void *v_out);
 
 #ifdef __cplusplus
 }

@@ -18,14 +18,19 @@ from burn_image_amd import workloads as W  # noqa: E402
 TORCH_DT = {"bf16": torch.bfloat16, "f16": torch.float16}
 ULP = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}  # one unit of the output, relative
 
-# (x dtype, output dtype, block, batch, tokens, q heads, kv heads, K, per-batch RoPE tables)
+# (x dtype, output dtype, block, batch, tokens, q heads, kv heads, K, per-batch RoPE tables,
+#  head-major outputs)
 CASES = [
     # 600 rows: two whole 256-row tiles and a ragged third; GQA 4:2
-    ("bf16", torch.float16, 128, 2, 300, 4, 2, 512, False),
+    ("bf16", torch.float16, 128, 2, 300, 4, 2, 512, False, False),
     # 3 + 2 heads: one tile holds a q and a k head, the last tile half lies past N; K % 64 == 32
-    ("f16", torch.bfloat16, 32, 1, 257, 3, 1, 352, False),
+    ("f16", torch.bfloat16, 32, 1, 257, 3, 1, 352, False, True),
     # 33 tokens: rows change batch inside an MFMA tile; cos / sin per (batch, token)
-    ("bf16", torch.float16, 64, 3, 33, 2, 2, 192, True),
+    ("bf16", torch.float16, 64, 3, 33, 2, 2, 192, True, False),
+    # the same with head-major outputs (the batch index enters the output offset)
+    ("bf16", torch.float16, 64, 3, 33, 2, 2, 192, True, True),
+    # GQA 4:2 head-major over two batches
+    ("f16", torch.float16, 128, 2, 300, 4, 2, 512, False, True),
 ]
 
 
@@ -52,7 +57,7 @@ def _within_one_unit(got, exp, dt, label, atol=2e-5):
 
 @pytest.mark.parametrize("case", range(len(CASES)))
 def test_gpu_fused_qkv_norm_rope_matches_two_calls_and_oracle(gpu, oracle, case):
-    xdt, odt, block, Bn, S, Hq, Hkv, K, per_batch = CASES[case]
+    xdt, odt, block, Bn, S, Hq, Hkv, K, per_batch, head_major = CASES[case]
     D = 128
     x, words, scales, gq, gk, cos, sin = _case_inputs(case, xdt, block, Bn, S, Hq, Hkv, K, per_batch)
     N = (Hq + 2 * Hkv) * D
@@ -60,7 +65,11 @@ def test_gpu_fused_qkv_norm_rope_matches_two_calls_and_oracle(gpu, oracle, case)
     xd = dev(x, TORCH_DT[xdt], gpu).reshape(Bn, S, K)
     nq, nk = B.RmsNorm(dev(gq, device=gpu), 1e-5), B.RmsNorm(dev(gk, device=gpu), 1e-6)
     rope = (dev(cos, device=gpu), dev(sin, device=gpu))
-    q1, k1, v1 = B.project_qkv_norm_rope(B.Linear(w), xd, nq, nk, rope, Hq, Hkv, D, out_dtype=odt)
+    q1, k1, v1 = B.project_qkv_norm_rope(B.Linear(w), xd, nq, nk, rope, Hq, Hkv, D, out_dtype=odt,
+                                         head_major=head_major)
+    if head_major:
+        assert tuple(q1.shape) == (Bn, Hq, S, D) and tuple(v1.shape) == (Bn, Hkv, S, D) and q1.is_contiguous()
+        q1, k1, v1 = (t.permute(0, 2, 1, 3) for t in (q1, k1, v1))
     assert q1.dtype == odt and tuple(q1.shape) == (Bn, S, Hq, D) and tuple(v1.shape) == (Bn, S, Hkv, D)
 
     # two calls: f32 projection, then the preparation kernel on its q / k / v views
