@@ -28,6 +28,8 @@
 // round of workgroups mostly idle, the tail tiles are split along K (SkPlan below).
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -227,6 +229,59 @@ __device__ __forceinline__ void store_tile_out(const floatx16_t (&acc)[G::WM][G:
           reinterpret_cast<_Float16 *>(yv)[row * N + col] = (_Float16)v;
         } else {
           reinterpret_cast<uint16_t *>(yv)[row * N + col] = (uint16_t)biq::f32_to_bf16_bits(v);
+        }
+      }
+  }
+}
+
+// The same epilogue without a branch per element: the output type is a template argument, and
+// each store goes through a buffer descriptor based at the wave's tile corner, with the row of the
+// register in the scalar offset and the lane's own row / column in the vector offset; an element
+// past M or N gets an out-of-range vector offset, so the hardware drops its store.  Used when
+// 32 WM rows of the output span less than 2^31 bytes (the offsets are 32-bit).
+template <class G, bool GLU, typename OT>
+__device__ __forceinline__ void store_tile_out_rows(const floatx16_t (&acc)[G::WM][G::WN], int64_t m0,
+                                                    int64_t n0, const float *__restrict__ bias,
+                                                    void *__restrict__ yv, int64_t M, int64_t N) {
+  constexpr int WM = G::WM, WN = G::WN;
+  constexpr uint32_t OOB = 0x80000000u;
+  constexpr uint32_t OSZ = sizeof(OT);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int64_t r0 = m0 + wm * (32 * WM);
+  const int64_t c0 = GLU ? n0 + wn * 32 : n0 + wn * (32 * WN);
+  const int64_t rows_left = M - r0, cols_left = N - c0;
+  OT *base = reinterpret_cast<OT *>(yv) + (r0 < M ? r0 : 0) * N + (c0 < N ? c0 : 0);
+  const int64_t bytes = (rows_left > 0 && cols_left > 0) ? ((rows_left - 1) * N + cols_left) * (int64_t)OSZ : 0;
+  const uint32_t n_rec = bytes > 0x7fffffffLL ? 0x7fffffffu : (uint32_t)bytes;
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)n_rec, 0x00020000);
+  const int64_t lim = rows_left - 4 * lh;  // register rows u (without 4 lh) below lim are inside M
+  const uint32_t row_bytes = (uint32_t)N * OSZ;
+#pragma unroll
+  for (int j = 0; j < (GLU ? 1 : WN); ++j) {
+    const int cl = GLU ? l32 : 32 * j + l32;  // column of the lane from c0
+    const bool col_ok = cl < cols_left;
+    const float bv = (!GLU && bias && col_ok) ? bias[c0 + cl] : 0.0f;
+    const uint32_t vo = col_ok ? (uint32_t)(4 * lh) * row_bytes + (uint32_t)cl * OSZ : OOB;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int u = 32 * i + 8 * (r >> 2) + (r & 3);
+        float v = acc[i][j][r] + bv;
+        if constexpr (GLU) {
+          // silu(a) = a / (1 + e^-a), times the W3 projection of the same row and column
+          v = v / (1.0f + __expf(-v)) * acc[i][1][r];
+        }
+        const uint32_t o = u < lim ? vo : OOB;
+        const uint32_t so = (uint32_t)u * row_bytes;
+        if constexpr (sizeof(OT) == 4) {
+          __builtin_amdgcn_raw_buffer_store_b32(biq::bitcast<uint32_t>(v), rs, o, so, 0);
+        } else if constexpr (std::is_same<OT, uint16_t>::value) {  // bf16 bits
+          __builtin_amdgcn_raw_buffer_store_b16((uint16_t)biq::f32_to_bf16_bits(v), rs, o, so, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b16(biq::bitcast<uint16_t>((_Float16)v), rs, o, so, 0);
         }
       }
   }
@@ -867,7 +922,14 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     continue;
   }
   if (ku0 == 0 && ku1 == units) {  // the whole K of the tile
-    store_tile_out<G, GLU>(acc, m0, n0, bias, yv, y_dtype, M, N);
+    // rows of a wave tile within 32-bit offsets (else the per-element form)
+    if ((int64_t)(32 * WM) * N * (y_dtype == BIQ_DTYPE_F32 ? 4 : 2) < (1LL << 31)) {
+      if (y_dtype == BIQ_DTYPE_F32) store_tile_out_rows<G, GLU, float>(acc, m0, n0, bias, yv, M, N);
+      else if (y_dtype == BIQ_DTYPE_F16) store_tile_out_rows<G, GLU, _Float16>(acc, m0, n0, bias, yv, M, N);
+      else store_tile_out_rows<G, GLU, uint16_t>(acc, m0, n0, bias, yv, M, N);
+    } else {
+      store_tile_out<G, GLU>(acc, m0, n0, bias, yv, y_dtype, M, N);
+    }
     continue;
   }
   // ---- tail chunk: the partial goes to slot c, register-major (element (register q, thread
