@@ -186,13 +186,16 @@ struct SkPlan {
 };
 
 // pid -> output tile: M-grouped raster (GROUP_M M tiles per group, walked column by column).
-__device__ __forceinline__ void tile_coords(int64_t pid, int tiles_m, int tiles_n, int64_t &tile_m,
-                                            int64_t &tile_n) {
-  const int64_t in_group = (int64_t)GROUP_M * tiles_n;
-  const int64_t first_m = (pid / in_group) * GROUP_M;
-  const int64_t gsize = (tiles_m - first_m) < GROUP_M ? (tiles_m - first_m) : GROUP_M;
-  tile_m = first_m + (pid % in_group) % gsize;
-  tile_n = (pid % in_group) / gsize;
+// (32-bit: tile counts stay below 2^31, host check; 64-bit divisions are long scalar sequences
+// that every wave of the workgroup would run)
+__device__ __forceinline__ void tile_coords(uint32_t pid, uint32_t tiles_m, uint32_t tiles_n,
+                                            int64_t &tile_m, int64_t &tile_n) {
+  const uint32_t in_group = (uint32_t)GROUP_M * tiles_n;
+  const uint32_t rem = pid % in_group;
+  const uint32_t first_m = (pid / in_group) * GROUP_M;
+  const uint32_t gsize = (tiles_m - first_m) < (uint32_t)GROUP_M ? (tiles_m - first_m) : (uint32_t)GROUP_M;
+  tile_m = first_m + rem % gsize;
+  tile_n = rem / gsize;
 }
 
 // Epilogue of one wave's accumulators: bias (or the SwiGLU gate), conversion, store.  Register r
@@ -475,7 +478,7 @@ __global__ void __launch_bounds__(RED_THREADS)
     if constexpr (GLU) g += *reinterpret_cast<const floatx4_t *>(src + (q + 16) * NT);
   }
   int64_t tile_m, tile_n;
-  tile_coords(dp_tiles + t, tiles_m, tiles_n, tile_m, tile_n);
+  tile_coords((uint32_t)(dp_tiles + t), (uint32_t)tiles_m, (uint32_t)tiles_n, tile_m, tile_n);
   const int64_t m0 = tile_m * G::BM, n0 = tile_n * BNO;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -526,29 +529,31 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   //      places workgroup L on XCD L % 8, and the workgroups of one XCD take a compact run of
   //      pids (tail workgroups likewise take a compact run of chunk indices; dp_tiles is a
   //      multiple of 8, so tail workgroup w also runs on XCD w % 8).
-  const int64_t T = (int64_t)tiles_m * tiles_n;
-  const int64_t L = blockIdx.x;
-  const int64_t units = sk.units;
-  const bool tail_wg = L >= sk.dp_tiles;
-  const int64_t tail = T - sk.dp_tiles, chunks = tail * sk.parts;
-  auto xcd_order = [](int64_t i, int64_t n) {
-    const int64_t q = n / 8, r = n % 8, xcd = i % 8, slot = i / 8;
+  // Work indices in 32 bits (tiles, chunks and K units stay below 2^31: host checks).
+  const uint32_t T = (uint32_t)tiles_m * (uint32_t)tiles_n;
+  const uint32_t L = blockIdx.x;
+  const uint32_t units = (uint32_t)sk.units, dp = (uint32_t)sk.dp_tiles, sk_wgs = (uint32_t)sk.sk_wgs;
+  const uint32_t parts = (uint32_t)sk.parts;
+  const bool tail_wg = L >= dp;
+  const uint32_t tail = T - dp, chunks = tail * parts;
+  auto xcd_order = [](uint32_t i, uint32_t n) {
+    const uint32_t q = n / 8, r = n % 8, xcd = i % 8, slot = i / 8;
     return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
   };
-  const int64_t first = tail_wg ? xcd_order(L - sk.dp_tiles, sk.sk_wgs) : xcd_order(L, sk.dp_tiles);
+  const uint32_t first = tail_wg ? xcd_order(L - dp, sk_wgs) : xcd_order(L, dp);
   // (the fused epilogue's launches own every tile: one segment, known at compile time, so no
   // value of the segment loop stays live through the epilogue)
-  const int64_t n_seg = EPI == 1 ? 1 : (tail_wg ? (chunks - first + sk.sk_wgs - 1) / sk.sk_wgs : 1);
+  const uint32_t n_seg = EPI == 1 ? 1u : (tail_wg ? (chunks - first + sk_wgs - 1) / sk_wgs : 1u);
 
-  for (int64_t seg = 0; seg < n_seg; ++seg) {
-  const int64_t c = first + seg * sk.sk_wgs;  // tail chunk (tail workgroups only)
-  const int64_t t_tail = tail_wg ? c % tail : 0, k_part = tail_wg ? c / tail : 0;
-  const int64_t pid = tail_wg ? sk.dp_tiles + t_tail : first;
+  for (uint32_t seg = 0; seg < n_seg; ++seg) {
+  const uint32_t c = first + seg * sk_wgs;  // tail chunk (tail workgroups only)
+  const uint32_t t_tail = tail_wg ? c % tail : 0u, k_part = tail_wg ? c / tail : 0u;
+  const uint32_t pid = tail_wg ? dp + t_tail : first;
   // with two register sets, tail parts start on even K tiles, so every part but the last (which
   // ends at K) has an even number of tiles for the paired loop below
-  constexpr int64_t GRAN = PART_GRANULE<G, LAYOUT, XMODE, BLK>;
-  auto part_start = [&](int64_t kp) {
-    return kp >= sk.parts ? units : GRAN * (kp * (units / GRAN) / sk.parts);
+  constexpr uint32_t GRAN = PART_GRANULE<G, LAYOUT, XMODE, BLK>;
+  auto part_start = [&](uint32_t kp) -> uint32_t {
+    return kp >= parts ? units : GRAN * (kp * (units / GRAN) / parts);
   };
   const int64_t ku0 = tail_wg ? part_start(k_part) : 0;
   const int64_t ku1 = tail_wg ? part_start(k_part + 1) : units;
@@ -936,7 +941,7 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   //      tid) at q * NT + tid: one coalesced 256-byte row per wave and register)
   {
     constexpr int PART = BM * BN;
-    const auto dst = __builtin_amdgcn_make_buffer_rsrc(sk.part + c * PART, 0, PART * 4, 0x00020000);
+    const auto dst = __builtin_amdgcn_make_buffer_rsrc(sk.part + (int64_t)c * PART, 0, PART * 4, 0x00020000);
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
