@@ -590,9 +590,21 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
   // load names its weight at compile time.  Otherwise both weights are read with the same offset,
   // the other weight's lanes passing an out-of-range offset (zero, no memory access), and the
   // two results are OR-ed -- which makes the wave wait for them right away.
+  // With an odd number (the 256 x 256 tile: one group per thread), the first half of the
+  // workgroup's waves loads W1 and the second half W3, so the weight is wave-uniform: the load
+  // picks its descriptor on the scalar unit (measured: the OR form made the fused SwiGLU's large
+  // tile wait for every word load right after issuing it).
   constexpr bool GLU_SPLIT = GLU && G::B_CHUNKS % 2 == 0;
+  constexpr bool GLU_WAVE = GLU && !GLU_SPLIT && LAYOUT == BIQ_Q4_KN_AXIS1 &&
+                            (BK / 8) * (BNO / 4) == G::B_CHUNKS * (NT / 2);
+  const bool half_w3 = __builtin_amdgcn_readfirstlane(tid / (NT / 2)) != 0;  // GLU_WAVE: W3 half
   auto kn_group = [&](int it, int &kwr, int &nc, bool &w3) {  // [K/8, N] word group `it`
-    if constexpr (GLU_SPLIT) {
+    if constexpr (GLU_WAVE) {
+      const int ch = tid % (NT / 2) + it * (NT / 2);
+      w3 = half_w3;
+      kwr = ch / (BNO / 4);
+      nc = (ch % (BNO / 4)) * 4;
+    } else if constexpr (GLU_SPLIT) {
       const int ch = tid + (it % (G::B_CHUNKS / 2)) * NT;
       w3 = it >= G::B_CHUNKS / 2;
       kwr = ch / (BNO / 4);
@@ -664,6 +676,7 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
     auto ld128 = [&](const __amdgpu_buffer_rsrc_t &r1, const __amdgpu_buffer_rsrc_t &r3, uint32_t off,
                      bool w3, int it) -> u32x4_t {
       if constexpr (!GLU) return __builtin_amdgcn_raw_buffer_load_b128(r1, off, 0, 0);
+      if constexpr (GLU_WAVE) return __builtin_amdgcn_raw_buffer_load_b128(half_w3 ? r3 : r1, off, 0, 0);
       if constexpr (GLU_SPLIT) return __builtin_amdgcn_raw_buffer_load_b128(it >= G::B_CHUNKS / 2 ? r3 : r1, off, 0, 0);
       return __builtin_amdgcn_raw_buffer_load_b128(r1, w3 ? OOB : off, 0, 0) |
              __builtin_amdgcn_raw_buffer_load_b128(r3, w3 ? off : OOB, 0, 0);
