@@ -2,7 +2,7 @@
 import numpy as np
 import torch
 
-# The north-star gate against the reference's f32 result.
+# The parity gate against the reference's f32 result: max |a - b| and mean|a - b| / mean|b|.
 MAX_ABS = 2e-3
 MEAN_REL = 1e-3
 
