@@ -497,8 +497,7 @@ __global__ void __launch_bounds__(64 * wg_waves(MASK), 8 / wg_waves(MASK)) attn_
         *reinterpret_cast<uint2 *>(dst) = w;
       } else {
         uint16_t *dst = reinterpret_cast<uint16_t *>(ob) + obase + d0;
-        uint2 w = make_uint2(biq::f32_to_bf16_bits(v0) | (biq::f32_to_bf16_bits(v1) << 16),
-                             biq::f32_to_bf16_bits(v2) | (biq::f32_to_bf16_bits(v3) << 16));
+        uint2 w = make_uint2(biq::pack_bf16x2(v0, v1), biq::pack_bf16x2(v2, v3));
         *reinterpret_cast<uint2 *>(dst) = w;
       }
     }

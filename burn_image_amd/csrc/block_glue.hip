@@ -162,8 +162,8 @@ __device__ __forceinline__ void store4(void *p, int64_t v, const f32x4_t &x) {
     reinterpret_cast<f32x4_t *>(p)[v] = x;
   } else if constexpr (DT == BIQ_DTYPE_BF16) {
     uint2 d;
-    d.x = biq::f32_to_bf16_bits(x[0]) | (biq::f32_to_bf16_bits(x[1]) << 16);
-    d.y = biq::f32_to_bf16_bits(x[2]) | (biq::f32_to_bf16_bits(x[3]) << 16);
+    d.x = biq::pack_bf16x2(x[0], x[1]);
+    d.y = biq::pack_bf16x2(x[2], x[3]);
     reinterpret_cast<uint2 *>(p)[v] = d;
   } else {
     uint2 d;

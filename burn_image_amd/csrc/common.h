@@ -59,12 +59,18 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   return (float)bitcast<_Float16>(h);
 }
 
-// Round-to-nearest-even f32 -> bf16 bits (finite inputs; NaN stays NaN).
+// Round-to-nearest-even f32 -> bf16 bits (NaN stays NaN): gfx950's v_cvt_pk_bf16_f32, equal to
+// the integer rounding (bits + 0x7fff + lsb) >> 16 for every finite input.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = bitcast<uint32_t>(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return bitcast<uint16_t>((__bf16)f);
+}
+
+// Two f32 -> packed bf16 pair (lo in bits 0-15), one conversion instruction.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+  f2_t v = {lo, hi};
+  return bitcast<uint32_t>(__builtin_convertvector(v, b2_t));
 }
 
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {

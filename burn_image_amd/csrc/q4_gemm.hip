@@ -417,7 +417,7 @@ __device__ __forceinline__ void qk_epilogue(const floatx16_t (&acc)[G::WM][G::WN
       }
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const uint32_t w = e.out_bf16 ? (biq::f32_to_bf16_bits(y[2 * c]) | (biq::f32_to_bf16_bits(y[2 * c + 1]) << 16))
+        const uint32_t w = e.out_bf16 ? biq::pack_bf16x2(y[2 * c], y[2 * c + 1])
                                       : biq::pack_f16x2(y[2 * c], y[2 * c + 1]);
         packed[i][ps][c >> 2][c & 3] = w;
       }

@@ -71,7 +71,7 @@ __device__ __forceinline__ float2 load_pair<bf16_t>(const bf16_t *p) {
 }
 
 __device__ __forceinline__ uint32_t store_bits(float a, float b, bool bf16) {
-  return bf16 ? (biq::f32_to_bf16_bits(a) | (biq::f32_to_bf16_bits(b) << 16)) : biq::pack_f16x2(a, b);
+  return bf16 ? biq::pack_bf16x2(a, b) : biq::pack_f16x2(a, b);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
