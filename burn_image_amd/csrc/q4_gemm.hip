@@ -294,7 +294,7 @@ __device__ __forceinline__ void store_tile_out_rows(const floatx16_t (&acc)[G::W
 // Hq + 2 Hkv heads of 128 (q heads, then k heads, then v heads); a 256 x 256 workgroup tile holds
 // two whole heads.  Per (token, q or k head), in the order of the fused preparation kernel for
 // f32 input (qk_prep.hip): rms = sqrt(sum x^2 / 128 + eps), n = (x / rms) * gamma (the quotient
-// correctly rounded: q = x * (1 / rms) and one residual step, Markstein), interleaved RoPE
+// correctly rounded from 1 / rms by one residual step, biq::div_rn), interleaved RoPE
 // y_2p = n_2p cos - n_2p+1 sin, y_2p+1 = n_2p+1 cos + n_2p sin, each product and sum rounded in
 // f32; then the cast.  v heads are only cast.  Outputs are contiguous [B, S, H, 128] or
 // [B, H, S, 128].  Only the sum of squares is added in another order than the preparation
@@ -398,14 +398,10 @@ __device__ __forceinline__ void qk_epilogue(const floatx16_t (&acc)[G::WM][G::WN
         ss = ss + __shfl_xor(ss, 1);
         ss = ss + __shfl_xor(ss, 2);
         ss = ss + __shfl_xor(ss, 4);
-        const float rms = sqrtf(ss / (float)D + eps);
-        const float inv = 1.0f / rms;
+        const float2 dv = biq::rn_divisor(sqrtf(ss / (float)D + eps));
         float n[16];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-          const float q = x[c] * inv;
-          n[c] = __builtin_fmaf(__builtin_fmaf(-q, rms, x[c]), inv, q) * gm[c];
-        }
+        for (int c = 0; c < 16; ++c) n[c] = biq::div_rn(x[c], dv.x, dv.y) * gm[c];
 #pragma unroll
         for (int c = 0; c < 16; c += 2) {
           y[c] = (n[c] * cs[c]) + ((-n[c + 1]) * sn[c]);

@@ -149,10 +149,10 @@ __global__ void __launch_bounds__(256) qk_prep_kernel(PrepArgs p, int out_bf16) 
     }
     const float sum_sq = wave_sum(x[i].x * x[i].x + x[i].y * x[i].y);  // wave-uniform
     const float eps = L.kind == 0 ? p.q_eps : p.k_eps;
-    const float rms = rnd<InT>(sqrtf(sum_sq / (float)p.D + eps));
+    const float2 dv = biq::rn_divisor(rnd<InT>(sqrtf(sum_sq / (float)p.D + eps)));
     const float *g = L.kind == 0 ? p.q_gamma : p.k_gamma;
-    const float n0 = active ? rnd<InT>(rnd<InT>(x[i].x / rms) * rnd<InT>(g[d])) : 0.0f;
-    const float n1 = active ? rnd<InT>(rnd<InT>(x[i].y / rms) * rnd<InT>(g[d + 1])) : 0.0f;
+    const float n0 = active ? rnd<InT>(rnd<InT>(biq::div_rn(x[i].x, dv.x, dv.y)) * rnd<InT>(g[d])) : 0.0f;
+    const float n1 = active ? rnd<InT>(rnd<InT>(biq::div_rn(x[i].y, dv.x, dv.y)) * rnd<InT>(g[d + 1])) : 0.0f;
     const float *cs = p.cos + L.b * p.rope_bs + L.s * p.D;
     const float *sn = p.sin + L.b * p.rope_bs + L.s * p.D;
     float y0 = 0.0f, y1 = 0.0f;
