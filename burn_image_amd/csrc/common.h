@@ -93,6 +93,15 @@ __device__ __forceinline__ float2 rn_divisor(float b) {
   return make_float2(inv == 0.0f ? 0.0f : b, inv);
 }
 
+// f32 -> f16 of the f32 value as it stands.  Without the empty asm, which only pins the value in
+// a register, the compiler folds a preceding multiply into the conversion (v_fma_mixlo_f16: the
+// exact product rounded once to f16), which differs from converting the f32 product wherever
+// that lands on an f16 tie; the reference rounds to f32 first.
+__device__ __forceinline__ _Float16 f16_of_f32(float v) {
+  asm("" : "+v"(v));
+  return (_Float16)v;
+}
+
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   half2_t h = {(_Float16)lo, (_Float16)hi};
   return bitcast<uint32_t>(h);

@@ -229,7 +229,7 @@ __device__ __forceinline__ void store_tile_out(const floatx16_t (&acc)[G::WM][G:
         if (y_dtype == BIQ_DTYPE_F32) {
           reinterpret_cast<float *>(yv)[row * N + col] = v;
         } else if (y_dtype == BIQ_DTYPE_F16) {
-          reinterpret_cast<_Float16 *>(yv)[row * N + col] = (_Float16)v;
+          reinterpret_cast<_Float16 *>(yv)[row * N + col] = biq::f16_of_f32(v);
         } else {
           reinterpret_cast<uint16_t *>(yv)[row * N + col] = (uint16_t)biq::f32_to_bf16_bits(v);
         }
@@ -284,7 +284,7 @@ __device__ __forceinline__ void store_tile_out_rows(const floatx16_t (&acc)[G::W
         } else if constexpr (std::is_same<OT, uint16_t>::value) {  // bf16 bits
           __builtin_amdgcn_raw_buffer_store_b16((uint16_t)biq::f32_to_bf16_bits(v), rs, o, so, 0);
         } else {
-          __builtin_amdgcn_raw_buffer_store_b16(biq::bitcast<uint16_t>((_Float16)v), rs, o, so, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(biq::bitcast<uint16_t>(biq::f16_of_f32(v)), rs, o, so, 0);
         }
       }
   }
@@ -488,7 +488,7 @@ __global__ void __launch_bounds__(RED_THREADS)
     if (y_dtype == BIQ_DTYPE_F32) {
       reinterpret_cast<float *>(yv)[row * N + col] = v;
     } else if (y_dtype == BIQ_DTYPE_F16) {
-      reinterpret_cast<_Float16 *>(yv)[row * N + col] = (_Float16)v;
+      reinterpret_cast<_Float16 *>(yv)[row * N + col] = biq::f16_of_f32(v);
     } else {
       reinterpret_cast<uint16_t *>(yv)[row * N + col] = (uint16_t)biq::f32_to_bf16_bits(v);
     }

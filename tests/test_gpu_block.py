@@ -64,6 +64,10 @@ def test_gpu_block_glue_residual_and_modulation(gpu, oracle, Wd):
                          next_scale=dev(scale, device=gpu), next_dtype=torch.bfloat16)
     assert nb16.dtype == torch.bfloat16
     assert np.max(np.abs(host(nb16).reshape(n0.shape) - n0)) <= np.max(np.abs(n0)) * 2.0 ** -8
+    # the bf16 output is the f32 one rounded once to nearest even (the hardware conversion)
+    nf32 = BL.block_glue(dev(x, device=gpu), next_norm=B.RmsNorm(dev(gn, device=gpu), 1e-5),
+                         next_scale=dev(scale, device=gpu), next_dtype=torch.float32)
+    assert np.array_equal(host(nb16).view(np.uint32), W.round_to_bf16(host(nf32)).view(np.uint32))
     # unmodulated residual (plain block, block.rs:113-131): no gate, bf16 branch
     br16 = W.round_to_bf16(br)
     r1, _ = glue_ref(oracle, x, br16, gb, 1e-5, None, None, 0, None, S)

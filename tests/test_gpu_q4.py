@@ -143,6 +143,10 @@ def test_gpu_q4_linear_bias_and_output_dtypes(gpu, oracle):
     assert np.max(np.abs(y16 - ref)) <= np.max(np.abs(ref)) * 2.0 ** -10
     yb = host(B.linear_forward(lin, xd, out_dtype=torch.bfloat16))
     assert np.max(np.abs(yb - ref)) <= np.max(np.abs(ref)) * 2.0 ** -7
+    # 16-bit outputs are the f32 result rounded once to nearest even, bit for bit
+    yf = host(B.linear_forward(lin, xd))
+    assert np.array_equal(yb.view(np.uint32), W.round_to_bf16(yf).view(np.uint32))
+    assert np.array_equal(y16, yf.astype(np.float16).astype(np.float32))
     # rank-3 input keeps its leading shape
     y3 = B.linear_forward(lin, xd[:128].reshape(2, 64, K))
     assert tuple(y3.shape) == (2, 64, N)
@@ -397,6 +401,9 @@ def test_gpu_q4_swiglu_feed_forward_and_dtypes(gpu, oracle):
     assert np.max(np.abs(g16 - gated)) <= np.max(np.abs(gated)) * 2.0 ** -10
     gb = host(B.q_matmul_swiglu(xd, lin[0].weight, lin[2].weight, out_dtype=torch.bfloat16))
     assert np.max(np.abs(gb - gated)) <= np.max(np.abs(gated)) * 2.0 ** -7
+    gf = host(B.q_matmul_swiglu(xd, lin[0].weight, lin[2].weight, out_dtype=torch.float32))
+    assert np.array_equal(gb.view(np.uint32), W.round_to_bf16(gf).view(np.uint32))
+    assert np.array_equal(g16, gf.astype(np.float16).astype(np.float32))
     with pytest.raises(B.InvalidArgument, match="share layout"):
         B.q_matmul_swiglu(xd, lin[0].weight, lin[1].weight)
 
