@@ -136,9 +136,13 @@ __global__ void __launch_bounds__(GT) block_glue_kernel(GlueArgs a) {
 // ---------------------------------------------------------------------------------------------
 // The same pass with the row held in registers (rows of up to 4096 elements, W % 4 == 0, 16-byte
 // aligned rows): one 256-thread workgroup per row, thread t holding the 4-vectors t, t + 256, ...
-// Every input of the row (branch, residual, modulation rows) is loaded up front with 16-byte
-// (f32) or 8-byte (16-bit) vector loads, so a row costs one memory round trip; the residual row r
-// stays in registers for the second norm.  Per element the arithmetic is the order of
+// Every load goes through a buffer descriptor at the row (or batch element) with no branch around
+// it -- vectors past the row and absent inputs read zero, and the null checks guard only the
+// arithmetic -- so each phase's loads (branch + residual + branch modulation; gamma + gate during
+// the first row sum; next gamma + scale during the second) are in flight together.  With the
+// loads under per-vector branches the compiler had waited after each residual load: three
+// serial memory round trips per row instead of one.  The residual row r stays in registers for
+// the second norm.  Per element the arithmetic is the order of
 // block_glue_kernel; only the f32 summation order of the two row sums differs.
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int GR_MAXK = 4;  // vectors of 4 per thread: rows up to 256 * 4 * 4 = 4096 elements
@@ -146,18 +150,29 @@ constexpr int GR_MAXK = 4;  // vectors of 4 per thread: rows up to 256 * 4 * 4 =
 // per thread in 92 registers (5 waves per SIMD) where the 4-vector form took 137-140 (3 waves);
 // measured on the 4608 x 3072 middle pass: 57 -> 48 us.
 
+// Buffer descriptor over `bytes` from base (a wave-uniform base): loads at offsets past the range
+// (or any offset, for a zero range) read as zero without a branch.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+
+// Elements 4v .. 4v + 3 of a row in dtype DT at byte offset o (one 16- or 8-byte load).
 template <int DT>
-__device__ __forceinline__ f32x4_t load4(const void *p, int64_t v) {  // elements 4v .. 4v + 3
+__device__ __forceinline__ f32x4_t load4(rsrc_t r, uint32_t o) {
   if constexpr (DT == BIQ_DTYPE_F32) {
-    return reinterpret_cast<const f32x4_t *>(p)[v];
+    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0);
+    return f32x4_t{biq::bitcast<float>(d[0]), biq::bitcast<float>(d[1]), biq::bitcast<float>(d[2]),
+                   biq::bitcast<float>(d[3])};
   } else {
-    const uint2 d = reinterpret_cast<const uint2 *>(p)[v];
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t d = __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0);
     if constexpr (DT == BIQ_DTYPE_BF16)
-      return f32x4_t{biq::bf16_lo_to_f32(d.x), biq::bf16_hi_to_f32(d.x), biq::bf16_lo_to_f32(d.y),
-                     biq::bf16_hi_to_f32(d.y)};
+      return f32x4_t{biq::bf16_lo_to_f32(d[0]), biq::bf16_hi_to_f32(d[0]), biq::bf16_lo_to_f32(d[1]),
+                     biq::bf16_hi_to_f32(d[1])};
     else
-      return f32x4_t{biq::f16_bits_to_f32((uint16_t)(d.x & 0xffffu)), biq::f16_bits_to_f32((uint16_t)(d.x >> 16)),
-                     biq::f16_bits_to_f32((uint16_t)(d.y & 0xffffu)), biq::f16_bits_to_f32((uint16_t)(d.y >> 16))};
+      return f32x4_t{biq::f16_bits_to_f32((uint16_t)(d[0] & 0xffffu)), biq::f16_bits_to_f32((uint16_t)(d[0] >> 16)),
+                     biq::f16_bits_to_f32((uint16_t)(d[1] & 0xffffu)), biq::f16_bits_to_f32((uint16_t)(d[1] >> 16))};
   }
 }
 
@@ -181,67 +196,98 @@ __device__ __forceinline__ void store4(void *p, int64_t v, const f32x4_t &x) {
 template <int BDT, int NDT, int GK>  // branch dtype; next dtype (-1: no next output); vectors per thread
 __global__ void __launch_bounds__(GT) block_glue_row_kernel(GlueArgs a) {
   __shared__ float red[GT / 64];
-  const int64_t row = blockIdx.x;
-  const int64_t b = row / a.rows_per_batch;
-  const int64_t W = a.width, nv = W / 4;
+  // rows < 2^31 (host check); a batch longer than the tensor holds every row
+  const uint32_t row = blockIdx.x;
+  const uint32_t rpb = (uint32_t)(a.rows_per_batch < a.rows ? a.rows_per_batch : a.rows);
+  const uint32_t b = row / rpb;
+  const uint32_t W = (uint32_t)a.width, nv = W / 4;  // W <= 4096: offsets within a row are small
   const float inv_w = 1.0f / (float)W;
-  const int64_t rv = row * nv, bv = b * nv;  // vector offsets of the row and of its batch rows
-  auto row4 = [](const float *p, int64_t v) { return reinterpret_cast<const f32x4_t *>(p)[v]; };
-  const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+  constexpr uint32_t BSZ = BDT == BIQ_DTYPE_F32 ? 16u : 8u;  // bytes per branch 4-vector
+  constexpr uint32_t OOB = 0x80000000u;
+  // descriptors at this row / this batch element (64-bit bases, wave-uniform); an absent input
+  // gets an empty range, so its loads read zero and only the arithmetic below is skipped
+  const int64_t rowW = (int64_t)row * W, bW = (int64_t)b * W;
+  const rsrc_t r_br = rsrc(static_cast<const char *>(a.branch) + rowW * (BSZ / 4), nv * BSZ);
+  auto vec_rsrc = [&](const float *p, int64_t first) { return rsrc(p ? p + first : a.x, p ? nv * 16u : 0u); };
+  const rsrc_t r_x = vec_rsrc(a.x, rowW);
+  const rsrc_t r_bsc = vec_rsrc(a.branch_scale, bW), r_bsh = vec_rsrc(a.branch_shift, bW);
+  const rsrc_t r_bg = vec_rsrc(a.branch_gamma, 0), r_gate = vec_rsrc(a.gate, bW);
+  const rsrc_t r_ng = vec_rsrc(a.next_gamma, 0), r_nsc = vec_rsrc(a.next_scale, bW);
+  auto vo = [&](int k) {  // byte offset of this thread's k-th 4-vector in an f32 row (OOB past W)
+    const uint32_t v = threadIdx.x + GT * k;
+    return v < nv ? v * 16u : OOB;
+  };
 
-  f32x4_t u[GK], xr[GK];  // the modulated branch (then r) and the residual input
+  // every load of the first phase in flight before the first use: the row's branch and residual
+  // vectors, then the branch modulation rows
+  f32x4_t u[GK], xr[GK], m0[GK], m1[GK];  // the modulated branch (then r); residual; scale; shift
 #pragma unroll
   for (int k = 0; k < GK; ++k) {
-    const int64_t v = threadIdx.x + GT * k;
-    const bool in = v < nv;
-    u[k] = in ? load4<BDT>(a.branch, rv + v) : z;
-    xr[k] = (in && a.x) ? row4(a.x, rv + v) : z;
+    const uint32_t v = threadIdx.x + GT * k;
+    u[k] = load4<BDT>(r_br, v < nv ? v * BSZ : OOB);
+    xr[k] = load4<BIQ_DTYPE_F32>(r_x, vo(k));
+  }
+#pragma unroll
+  for (int k = 0; k < GK; ++k) {
+    m0[k] = load4<BIQ_DTYPE_F32>(r_bsc, vo(k));
+    m1[k] = load4<BIQ_DTYPE_F32>(r_bsh, vo(k));
   }
   float ss = 0.0f;
 #pragma unroll
   for (int k = 0; k < GK; ++k) {
-    const int64_t v = threadIdx.x + GT * k;
-    if (v < nv) {
-      if (a.branch_scale) u[k] *= row4(a.branch_scale, bv + v) + 1.0f;
-      if (a.branch_shift) u[k] += row4(a.branch_shift, bv + v);
+    if (threadIdx.x + GT * k < nv) {
+      if (a.branch_scale) u[k] *= m0[k] + 1.0f;
+      if (a.branch_shift) u[k] += m1[k];
       ss += u[k][0] * u[k][0] + u[k][1] * u[k][1] + u[k][2] * u[k][2] + u[k][3] * u[k][3];
     }
   }
   float ss_r = ss;
   if (a.x) {
+    // gamma and gate rows in flight during the row sum
+#pragma unroll
+    for (int k = 0; k < GK; ++k) {
+      m0[k] = load4<BIQ_DTYPE_F32>(r_bg, vo(k));
+      m1[k] = load4<BIQ_DTYPE_F32>(r_gate, vo(k));
+    }
     const float2 db = biq::rn_divisor(sqrtf(block_sum(ss, red) * inv_w + a.branch_eps));
     ss_r = 0.0f;
 #pragma unroll
     for (int k = 0; k < GK; ++k) {
-      const int64_t v = threadIdx.x + GT * k;
+      const uint32_t v = threadIdx.x + GT * k;
       if (v < nv) {
         f32x4_t nb;
 #pragma unroll
         for (int e = 0; e < 4; ++e) nb[e] = biq::div_rn(u[k][e], db.x, db.y);
-        if (a.branch_gamma) nb *= row4(a.branch_gamma, v);
+        if (a.branch_gamma) nb *= m0[k];
         if (a.gate) {
-          const f32x4_t gt = row4(a.gate, bv + v);
+          const f32x4_t gt = m1[k];
           nb *= f32x4_t{tanhf(gt[0]), tanhf(gt[1]), tanhf(gt[2]), tanhf(gt[3])};
         }
         const f32x4_t r = xr[k] + nb;
-        if (a.x_out) reinterpret_cast<f32x4_t *>(a.x_out)[rv + v] = r;
+        if (a.x_out) reinterpret_cast<f32x4_t *>(a.x_out)[rowW / 4 + v] = r;
         u[k] = r;
         ss_r += r[0] * r[0] + r[1] * r[1] + r[2] * r[2] + r[3] * r[3];
       }
     }
   }
   if constexpr (NDT >= 0) {
+    // next gamma and scale rows in flight during the second row sum
+#pragma unroll
+    for (int k = 0; k < GK; ++k) {
+      m0[k] = load4<BIQ_DTYPE_F32>(r_ng, vo(k));
+      m1[k] = load4<BIQ_DTYPE_F32>(r_nsc, vo(k));
+    }
     const float2 dr = biq::rn_divisor(sqrtf(block_sum(ss_r, red) * inv_w + a.next_eps));
 #pragma unroll
     for (int k = 0; k < GK; ++k) {
-      const int64_t v = threadIdx.x + GT * k;
+      const uint32_t v = threadIdx.x + GT * k;
       if (v < nv) {
         f32x4_t n;
 #pragma unroll
         for (int e = 0; e < 4; ++e) n[e] = biq::div_rn(u[k][e], dr.x, dr.y);
-        if (a.next_gamma) n *= row4(a.next_gamma, v);
-        if (a.next_scale) n *= row4(a.next_scale, bv + v) + 1.0f;
-        store4<NDT>(a.next_out, rv + v, n);
+        if (a.next_gamma) n *= m0[k];
+        if (a.next_scale) n *= m1[k] + 1.0f;
+        store4<NDT>(a.next_out, rowW / 4 + v, n);
       }
     }
   }
