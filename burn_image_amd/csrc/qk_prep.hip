@@ -52,22 +52,17 @@ __device__ __forceinline__ float rnd(float v) {
   }
 }
 
-template <typename T>
-__device__ __forceinline__ float2 load_pair(const T *p);
-template <>
-__device__ __forceinline__ float2 load_pair<float>(const float *p) {
+__device__ __forceinline__ float2 load_pair(const float *p) {
   return *reinterpret_cast<const float2 *>(p);
 }
-template <>
-__device__ __forceinline__ float2 load_pair<f16_t>(const f16_t *p) {
-  const uint32_t w = *reinterpret_cast<const uint32_t *>(p);
-  return make_float2(biq::f16_bits_to_f32((uint16_t)(w & 0xffffu)),
-                     biq::f16_bits_to_f32((uint16_t)(w >> 16)));
-}
-template <>
-__device__ __forceinline__ float2 load_pair<bf16_t>(const bf16_t *p) {
-  const uint32_t w = *reinterpret_cast<const uint32_t *>(p);
-  return make_float2(biq::bf16_lo_to_f32(w), biq::bf16_hi_to_f32(w));
+// Two 16-bit elements (one 32-bit word, low half first) widened to f32.
+template <typename T>
+__device__ __forceinline__ float2 widen_pair(uint32_t w) {
+  if constexpr (std::is_same<T, f16_t>::value)
+    return make_float2(biq::f16_bits_to_f32((uint16_t)(w & 0xffffu)),
+                       biq::f16_bits_to_f32((uint16_t)(w >> 16)));
+  else
+    return make_float2(biq::bf16_lo_to_f32(w), biq::bf16_hi_to_f32(w));
 }
 
 __device__ __forceinline__ uint32_t store_bits(float a, float b, bool bf16) {
@@ -124,17 +119,29 @@ __global__ void __launch_bounds__(256) qk_prep_kernel(PrepArgs p, int out_bf16) 
 
   RowLoc L0 = locate(p, wave * PREP_ROWS);
   RowLoc L = L0;
+  // 16-bit inputs are loaded as raw words and widened after the loop: with the widening inside
+  // the conditional load the compiler waited for each row's load in turn (8 serial round trips)
+  constexpr bool WIDE = sizeof(InT) == 4;
   float2 x[PREP_ROWS];
+  [[maybe_unused]] uint32_t w[PREP_ROWS];
 #pragma unroll
   for (int i = 0; i < PREP_ROWS; ++i) {
     x[i] = make_float2(0.0f, 0.0f);
+    if constexpr (!WIDE) w[i] = 0u;
     if (L.kind < 3) {
       const int64_t *st = L.kind == 0 ? p.qs : (L.kind == 1 ? p.ks : p.vs);
       const InT *src = reinterpret_cast<const InT *>(L.kind == 0 ? p.q : (L.kind == 1 ? p.k : p.v)) +
                        L.b * st[0] + L.s * st[1] + L.h * st[2];
-      if (active) x[i] = load_pair<InT>(src + d);
+      if (active) {
+        if constexpr (WIDE) x[i] = load_pair(src + d);
+        else w[i] = *reinterpret_cast<const uint32_t *>(src + d);
+      }
     }
     advance(p, L);
+  }
+  if constexpr (!WIDE) {
+#pragma unroll
+    for (int i = 0; i < PREP_ROWS; ++i) x[i] = widen_pair<InT>(w[i]);
   }
 
   L = L0;
