@@ -193,7 +193,10 @@ __device__ __forceinline__ void store4(void *p, int64_t v, const f32x4_t &x) {
   }
 }
 
-template <int BDT, int NDT, int GK>  // branch dtype; next dtype (-1: no next output); vectors per thread
+// branch dtype; next dtype (-1: no next output); vectors per thread; residual given (a.x): the
+// first norm of a block has none, and its instantiation without the residual's registers runs
+// more waves per SIMD
+template <int BDT, int NDT, int GK, bool RES>
 __global__ void __launch_bounds__(GT) block_glue_row_kernel(GlueArgs a) {
   __shared__ float red[GT / 64];
   // rows < 2^31 (host check); a batch longer than the tensor holds every row
@@ -225,7 +228,7 @@ __global__ void __launch_bounds__(GT) block_glue_row_kernel(GlueArgs a) {
   for (int k = 0; k < GK; ++k) {
     const uint32_t v = threadIdx.x + GT * k;
     u[k] = load4<BDT>(r_br, v < nv ? v * BSZ : OOB);
-    xr[k] = load4<BIQ_DTYPE_F32>(r_x, vo(k));
+    if constexpr (RES) xr[k] = load4<BIQ_DTYPE_F32>(r_x, vo(k));
   }
 #pragma unroll
   for (int k = 0; k < GK; ++k) {
@@ -242,7 +245,7 @@ __global__ void __launch_bounds__(GT) block_glue_row_kernel(GlueArgs a) {
     }
   }
   float ss_r = ss;
-  if (a.x) {
+  if constexpr (RES) {
     // gamma and gate rows in flight during the row sum
 #pragma unroll
     for (int k = 0; k < GK; ++k) {
@@ -327,16 +330,21 @@ extern "C" int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t
   if (vec) {
     const dim3 grid((unsigned)rows);
     const int gk = (int)((width / 4 + GT - 1) / GT);
+#define BIQ_GLUE_K(BD, ND, RES)                                                                    \
+  do {                                                                                             \
+    if (gk == 1) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 1, RES>), grid, dim3(GT), 0, s, a); \
+    else if (gk == 2) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 2, RES>), grid, dim3(GT), 0, s, a); \
+    else if (gk == 3) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 3, RES>), grid, dim3(GT), 0, s, a); \
+    else hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 4, RES>), grid, dim3(GT), 0, s, a);     \
+  } while (0)
 #define BIQ_GLUE(BD, ND)                                                                           \
   do {                                                                                             \
-    if (gk == 1) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 1>), grid, dim3(GT), 0, s, a);  \
-    else if (gk == 2) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 2>), grid, dim3(GT), 0, s, a); \
-    else if (gk == 3) hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 3>), grid, dim3(GT), 0, s, a); \
-    else hipLaunchKernelGGL((block_glue_row_kernel<BD, ND, 4>), grid, dim3(GT), 0, s, a);          \
+    if (x) BIQ_GLUE_K(BD, ND, true);                                                               \
+    else BIQ_GLUE_K(BD, ND, false);                                                                \
   } while (0)
 #define BIQ_GLUE_N(BD)                                                                             \
   do {                                                                                             \
-    if (!next_out) BIQ_GLUE(BD, -1);                                                               \
+    if (!next_out) BIQ_GLUE_K(BD, -1, true);  /* (x is given: checked above) */                    \
     else if (next_dtype == BIQ_DTYPE_F32) BIQ_GLUE(BD, BIQ_DTYPE_F32);                             \
     else if (next_dtype == BIQ_DTYPE_F16) BIQ_GLUE(BD, BIQ_DTYPE_F16);                             \
     else BIQ_GLUE(BD, BIQ_DTYPE_BF16);                                                             \
@@ -346,6 +354,7 @@ extern "C" int biq_block_glue(void *stream, int64_t rows, int64_t width, int64_t
     else BIQ_GLUE_N(BIQ_DTYPE_BF16);
 #undef BIQ_GLUE_N
 #undef BIQ_GLUE
+#undef BIQ_GLUE_K
     return biq::check_launch("block glue");
   }
   hipLaunchKernelGGL(block_glue_kernel, dim3((unsigned)rows), dim3(GT), 0, s, a);
