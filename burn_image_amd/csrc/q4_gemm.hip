@@ -34,7 +34,9 @@
 
 namespace {
 
-constexpr int GROUP_M = 8;    // M tiles per raster group
+// M tiles per raster group (measured on the 4608-row projections against 2, 3, 6, 8 and 16: 4 and
+// 2 lead 8 by 0.3-1%, 16 trails)
+constexpr int GROUP_M = 4;
 
 enum XMode { XM_F16 = 0, XM_BF16 = 1, XM_F32 = 2 };
 
