@@ -913,12 +913,14 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
       }
       if constexpr (STAGE_LATE) stage_next();
       if constexpr (RESC) {
-        // One MFMA, then six VALU, through the tile: otherwise the block-boundary rescale (one
-        // multiply per accumulator) runs as a burst before the block's first MFMA.
+        // One MFMA, then four VALU, through the tile: otherwise the block-boundary rescale (one
+        // multiply per accumulator) runs as a burst before the block's first MFMA.  (Same-box
+        // runs of 2-10 VALU per MFMA: 4 leads 6 by ~0.5% summed over the 4608-row projections,
+        // 8 and 10 trail.)
 #pragma unroll
         for (int g = 0; g < BK / 16 * WM * WN; ++g) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
         }
       }
       __syncthreads();
