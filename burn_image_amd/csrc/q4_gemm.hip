@@ -912,6 +912,16 @@ __global__ void __launch_bounds__(G::NTHREADS, G::NTHREADS >= 512 ? 1 : 2)
         }
       }
       if constexpr (STAGE_LATE) stage_next();
+      if constexpr (!RESC && XMODE != XM_F32 && BLK >= 32) {
+        // 128 x 256 tile: one MFMA, then six VALU (the block-end flush and the decode of the next
+        // fragments spread through the MFMA stream; same-box runs: ~0.6% over the shapes that
+        // take this tile, up to 2%)
+#pragma unroll
+        for (int g = 0; g < BK / 16 * WM * WN; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+        }
+      }
       if constexpr (RESC) {
         // One MFMA, then four VALU, through the tile: otherwise the block-boundary rescale (one
         // multiply per accumulator) runs as a burst before the block's first MFMA.  (Same-box
