@@ -53,6 +53,11 @@ constexpr int KN_SLAB = 64;      // columns per wave, [K/8, N] layout
 #define BIQ_GEMV_KN_BATCH 4
 #endif
 constexpr int KN_BATCH = BIQ_GEMV_KN_BATCH;  // steps of 32 k per batch (>= 4: a unit of >= 128 k)
+// The in-register [K/8, N] kernel takes twice that for blocks >= 32: twice the loads in flight per
+// wave (16 x 3072 x 9216: 9.44 -> 9.04 us); the LDS-staged kernel keeps KN_BATCH (8 measured
+// slower there: 7.4 -> 8.3 us at 1 x 3072 x 12288), and so do blocks of 8 and 16, whose scales per
+// batch would grow with it.
+constexpr int kn_reg_batch(int blk) { return blk >= 32 ? 2 * KN_BATCH : KN_BATCH; }
 constexpr int NK_SLAB = 16;      // columns per wave, [N, K/8] layout
 constexpr int NK_BATCH = 2;      // super-steps of 128 k per batch -> unit of 256 k
 
@@ -216,13 +221,14 @@ __global__ void __launch_bounds__(WPS > 1 ? 64 * WPS : GV_THREADS) q4_gemv_kn_ke
   const bool col_ok = ncol < N;
   const bool row_ok = c16 < M;
   constexpr int ESZ = XD == BIQ_DTYPE_F32 ? 4 : 2;
+  constexpr int KB = kn_reg_batch(BLK);  // steps of 32 k per batch
 
   f32x4_t acc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   constexpr int SPB = BLK >= 32 ? BLK / 32 : 1;                                        // steps per block
-  constexpr int NSC = BLK >= 32 ? (KN_BATCH + SPB - 1) / SPB : KN_BATCH * (32 / BLK);  // blocks per batch
+  constexpr int NSC = BLK >= 32 ? (KB + SPB - 1) / SPB : KB * (32 / BLK);  // blocks per batch
 
   // Branch-free loads through buffer descriptors (scalar: every base is wave-uniform): words and
   // scales through descriptors that start at the batch and end at the matrix, activations through
@@ -230,7 +236,8 @@ __global__ void __launch_bounds__(WPS > 1 ? 64 * WPS : GV_THREADS) q4_gemv_kn_ke
   // columns past N) reads as zero; an activation past K or M gets the out-of-range offset OOB and
   // reads as zero.  Without a branch per load the compiler waits for each step's data only when
   // that step computes, so a batch's loads overlap its earlier steps.  Offsets are 32-bit: inside
-  // a batch below 16 packed rows of N < 2^24 words; activations below 16 rows of ldx < 2^21.
+  // a batch below 32 packed rows of N < 2^24 words (32 N * 4 < 2^31); activations below 16 rows
+  // of ldx < 2^21.
   constexpr uint32_t OOB = 0x80000000u;
   auto rsrc = [](const void *base, int64_t bytes) {
     const uint32_t n = bytes > 0x7fffffffLL ? 0x7fffffffu : (bytes < 0 ? 0u : (uint32_t)bytes);
@@ -239,15 +246,15 @@ __global__ void __launch_bounds__(WPS > 1 ? 64 * WPS : GV_THREADS) q4_gemv_kn_ke
   const auto rx = rsrc(xv, ((M - 1) * ldx + K) * ESZ);
   const uint32_t w_lane = col_ok ? (uint32_t)((g * N + ncol) * 4) : OOB;
   const int64_t x_row = (int64_t)c16 * ldx + 8 * g;  // this lane's 8 activations of a step, less kb
-  // K chunk c is the units of 32 * KN_BATCH k numbered c, c + nchunks, c + 2 nchunks, ...: the
+  // K chunk c is the units of 32 * KB k numbered c, c + nchunks, c + 2 nchunks, ...: the
   // chunks of a slab interleave, so the waves of the chip read one band of packed rows at a time.
-  for (int64_t kb = chunk * 32 * KN_BATCH; kb < K; kb += nchunks * 32 * KN_BATCH) {
+  for (int64_t kb = chunk * 32 * KB; kb < K; kb += nchunks * 32 * KB) {
     const int64_t kw0 = kb / 8;
     const auto rw = rsrc(words + kw0 * N, (KW - kw0) * N * 4);
-    u32x4_t wv[KN_BATCH];
-    XRaw<XD> xr[KN_BATCH];
+    u32x4_t wv[KB];
+    XRaw<XD> xr[KB];
 #pragma unroll
-    for (int t = 0; t < KN_BATCH; ++t) {
+    for (int t = 0; t < KB; ++t) {
       wv[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_lane == OOB ? OOB : w_lane + (uint32_t)(4 * t * N * 4), 0, 0);
       const bool x_ok = row_ok && kb + 32 * t + 8 * g < K;
       const uint32_t xo = x_ok ? (uint32_t)((x_row + kb + 32 * t) * ESZ) : OOB;
@@ -275,7 +282,7 @@ __global__ void __launch_bounds__(WPS > 1 ? 64 * WPS : GV_THREADS) q4_gemv_kn_ke
     if constexpr (BLK >= 32) {
       f32x4_t p[4];
 #pragma unroll
-      for (int t = 0; t < KN_BATCH; ++t) {
+      for (int t = 0; t < KB; ++t) {
         half8_t ahi, alo;
         x8_slots<XD>(xr[t], ahi, alo);
 #pragma unroll
@@ -291,7 +298,7 @@ __global__ void __launch_bounds__(WPS > 1 ? 64 * WPS : GV_THREADS) q4_gemv_kn_ke
       constexpr int PER = 32 / BLK, GPB = BLK / 8;
       const half8_t zh = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-      for (int t = 0; t < KN_BATCH; ++t) {
+      for (int t = 0; t < KB; ++t) {
         half8_t ahi, alo;
         x8_slots<XD>(xr[t], ahi, alo);
 #pragma unroll
@@ -705,9 +712,12 @@ int q4_gemv_launch(hipStream_t s, const void *x, int x_dtype, int64_t M, int64_t
   // of 8 or 16, whose decode needs more than the 128 registers a 1024-thread workgroup leaves --
   // and at least one unit each).  Taken when the slabs times the chunks give enough waves to
   // stream the weights.
+  // (units of the in-register kernels from here on)
+  const int64_t unit_r = kn ? 32 * kn_reg_batch(block) : unit;
+  const int64_t kunits_r = (K + unit_r - 1) / unit_r;
   const int64_t max_wps = block <= 16 ? 8 : 16;
-  int64_t wps_chunks = (kunits + max_wps - 1) / max_wps;      // units per chunk
-  const int64_t nchunks_wg = (kunits + wps_chunks - 1) / wps_chunks;
+  int64_t wps_chunks = (kunits_r + max_wps - 1) / max_wps;      // units per chunk
+  const int64_t nchunks_wg = (kunits_r + wps_chunks - 1) / wps_chunks;
   if (nslabs * nchunks_wg >= 1024 && nslabs <= 0x7fffffffLL) {
     const int wps = nchunks_wg <= 4 ? 4 : (nchunks_wg <= 8 ? 8 : (nchunks_wg <= 12 ? 12 : 16));
     const dim3 grid((unsigned)nslabs);
@@ -746,7 +756,7 @@ int q4_gemv_launch(hipStream_t s, const void *x, int x_dtype, int64_t M, int64_t
 
   // Across workgroups: split K until about BIQ_GEMV_TARGET_WAVES waves stream the weights.
   int64_t ksplit = (BIQ_GEMV_TARGET_WAVES + nslabs - 1) / nslabs;
-  if (ksplit > kunits) ksplit = kunits;
+  if (ksplit > kunits_r) ksplit = kunits_r;
   if (ksplit < 1) ksplit = 1;
   // partial rows cost ksplit * M * N floats of workspace: keep them under 256 MB
   const int64_t max_split = (int64_t)(256 << 20) / (4 * M * N);
